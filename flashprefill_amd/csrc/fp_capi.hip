@@ -1,0 +1,311 @@
+// C ABI of the FlashPrefill gfx950 path: argument validation, workspace
+// layout and the launch sequence plan -> pool -> search -> attention. All
+// launches go to the caller's stream; nothing here allocates or synchronises
+// (except fp_read_status, which is documented to).
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "fp_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(FP_E_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+}
+
+size_t align_up(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int validate(const fp_problem* p) {
+  if (!p) return fail(FP_E_INVALID_ARG, "problem descriptor is NULL");
+  if (!p->q || !p->k || !p->v || !p->o) return fail(FP_E_INVALID_ARG, "q/k/v/o must be non-NULL");
+  if (p->dtype != FP_DTYPE_BF16 && p->dtype != FP_DTYPE_F16)
+    return fail(FP_E_UNSUPPORTED, "dtype %d unsupported (bf16 or fp16 only)", p->dtype);
+  if (p->head_dim != 64 && p->head_dim != 128)
+    return fail(FP_E_UNSUPPORTED, "head_dim %d unsupported (64 or 128)", p->head_dim);
+  if (p->block_size != fp::kBlock)
+    return fail(FP_E_UNSUPPORTED, "block_size %d unsupported (128)", p->block_size);
+  if (p->num_q_heads < 1 || p->num_kv_heads < 1 || p->num_q_heads % p->num_kv_heads)
+    return fail(FP_E_INVALID_ARG, "num_q_heads (%d) must be a positive multiple of num_kv_heads (%d)",
+                p->num_q_heads, p->num_kv_heads);
+  if (p->batch < 1 || p->batch > fp::kMaxBatch)
+    return fail(FP_E_INVALID_ARG, "batch %d outside [1, %d]", p->batch, fp::kMaxBatch);
+  if (p->max_seq_len < 1 || p->max_seq_len > fp::kMaxBlocks * fp::kBlock)
+    return fail(FP_E_INVALID_ARG, "max_seq_len %d outside [1, %d]", p->max_seq_len,
+                fp::kMaxBlocks * fp::kBlock);
+  if (p->total_tokens < 0) return fail(FP_E_INVALID_ARG, "total_tokens < 0");
+  if (!p->cu_seqlens) {
+    if (p->uniform_seq_len < 0 || p->uniform_seq_len > p->max_seq_len)
+      return fail(FP_E_INVALID_ARG, "uniform_seq_len %d outside [0, max_seq_len]", p->uniform_seq_len);
+    if (static_cast<int64_t>(p->batch) * p->uniform_seq_len > p->total_tokens)
+      return fail(FP_E_INVALID_ARG, "batch * uniform_seq_len exceeds total_tokens");
+  }
+  if (!aligned16(p->q) || !aligned16(p->k) || !aligned16(p->v) || !aligned16(p->o))
+    return fail(FP_E_INVALID_ARG, "q/k/v/o must be 16-byte aligned");
+  const int64_t strides[8] = {p->q_stride_tok, p->q_stride_head, p->k_stride_tok, p->k_stride_head,
+                              p->v_stride_tok, p->v_stride_head, p->o_stride_tok, p->o_stride_head};
+  for (int s = 0; s < 8; ++s)
+    if (strides[s] < 0 || strides[s] % 8)
+      return fail(FP_E_INVALID_ARG, "strides must be non-negative multiples of 8 elements");
+  if (p->min_budget < 0) return fail(FP_E_INVALID_ARG, "min_budget < 0");
+  if (p->min_budget > 0)
+    return fail(FP_E_UNSUPPORTED, "min_budget > 0 is not implemented on the GPU path");
+  if (p->native_normalize != 0 && p->native_normalize != 1)
+    return fail(FP_E_INVALID_ARG, "native_normalize must be 0 or 1");
+  return FP_OK;
+}
+
+int layout(const fp_problem* p, fp_ws_layout* L) {
+  const int rc = validate(p);
+  if (rc != FP_OK) return rc;
+  memset(L, 0, sizeof(*L));
+  const int64_t B = p->batch;
+  const int64_t nb_max = (p->max_seq_len + fp::kBlock - 1) / fp::kBlock;
+  int64_t cap = (p->total_tokens + (fp::kBlock - 1) * B) / fp::kBlock;
+  if (cap > B * nb_max) cap = B * nb_max;
+  if (cap < 1) cap = 1;
+  const int64_t full = cap / nb_max, rem = cap % nb_max;
+  const int64_t tri = full * nb_max * (nb_max + 1) / 2 + rem * (rem + 1) / 2;
+  L->nb_max = static_cast<int32_t>(nb_max);
+  L->nb_sum_cap = cap;
+  L->tri_cap = tri;
+  const int64_t Hq = p->num_q_heads, Hkv = p->num_kv_heads, d = p->head_dim;
+  if (Hq * cap > (int64_t(1) << 31)) return fail(FP_E_INVALID_ARG, "too many work items");
+  size_t off = 0;
+  L->status_off = off;     off = align_up(off + 4);
+  L->seq_tile_off = off;   off = align_up(off + 8 * (B + 1));
+  L->seq_tri_off = off;    off = align_up(off + 8 * (B + 1));
+  L->seq_start_off = off;  off = align_up(off + 8 * B);
+  L->seq_len_off = off;    off = align_up(off + 4 * B);
+  L->items_off = off;      off = align_up(off + 8 * cap);
+  L->mk_off = off;         off = align_up(off + 2 * cap * Hkv * d);
+  L->cnt_off = off;        off = align_up(off + 4 * Hq * cap);
+  L->idx_off = off;        off = align_up(off + 4 * Hq * tri);
+  L->total_bytes = off;
+  return FP_OK;
+}
+
+fp::SeqTables tables(const fp_ws_layout& L, void* ws) {
+  char* base = static_cast<char*>(ws);
+  fp::SeqTables t;
+  t.status = reinterpret_cast<uint32_t*>(base + L.status_off);
+  t.seq_tile = reinterpret_cast<int64_t*>(base + L.seq_tile_off);
+  t.seq_tri = reinterpret_cast<int64_t*>(base + L.seq_tri_off);
+  t.seq_start = reinterpret_cast<int64_t*>(base + L.seq_start_off);
+  t.seq_len = reinterpret_cast<int32_t*>(base + L.seq_len_off);
+  t.items = reinterpret_cast<int32_t*>(base + L.items_off);
+  return t;
+}
+
+float sm_scale_log2(int head_dim) {
+  // fp32(1/sqrt(d)) * fp32(log2 e) in fp32, as the reference kernels compute it
+  const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(head_dim)));
+  const float log2e = static_cast<float>(1.4426950408889634);
+  volatile float prod = scale * log2e;
+  return prod;
+}
+
+int prepare(const fp_problem* p, void* ws, fp_ws_layout* L) {
+  const int rc = layout(p, L);
+  if (rc != FP_OK) return rc;
+  if (!ws) return fail(FP_E_INVALID_ARG, "workspace is NULL");
+  if (!aligned16(ws)) return fail(FP_E_INVALID_ARG, "workspace must be 16-byte aligned");
+  return FP_OK;
+}
+
+int run_plan(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s) {
+  fp::PlanArgs a;
+  a.tab = tables(L, ws);
+  a.cu = p->cu_seqlens;
+  a.B = p->batch;
+  a.uniform_len = p->uniform_seq_len;
+  a.max_seq_len = p->max_seq_len;
+  a.nb_max = L.nb_max;
+  a.total_tokens = p->total_tokens;
+  const hipError_t e = fp::launch_plan(a, s);
+  return e == hipSuccess ? FP_OK : hip_fail(e, "plan launch");
+}
+
+int run_pool(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s) {
+  fp::PoolArgs a;
+  a.tab = tables(L, ws);
+  a.k = static_cast<const uint16_t*>(p->k);
+  a.kst = p->k_stride_tok;
+  a.khs = p->k_stride_head;
+  a.mk = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + L.mk_off);
+  a.B = p->batch;
+  a.Hkv = p->num_kv_heads;
+  const hipError_t e = fp::launch_pool(a, p->dtype, p->head_dim, L.nb_sum_cap, s);
+  return e == hipSuccess ? FP_OK : hip_fail(e, "pool launch");
+}
+
+fp::SearchArgs search_args(const fp_problem* p, const fp_ws_layout& L, void* ws) {
+  fp::SearchArgs a;
+  memset(&a, 0, sizeof(a));
+  char* base = static_cast<char*>(ws);
+  a.tab = tables(L, ws);
+  a.q = static_cast<const uint16_t*>(p->q);
+  a.qst = p->q_stride_tok;
+  a.qhs = p->q_stride_head;
+  a.mk = reinterpret_cast<const uint16_t*>(base + L.mk_off);
+  a.idx = reinterpret_cast<int32_t*>(base + L.idx_off);
+  a.cnt = reinterpret_cast<int32_t*>(base + L.cnt_off);
+  a.tri_cap = L.tri_cap;
+  a.nb_sum_cap = L.nb_sum_cap;
+  a.B = p->batch;
+  a.Hq = p->num_q_heads;
+  a.Hkv = p->num_kv_heads;
+  a.nb_max = L.nb_max;
+  a.sm_scale_log2 = sm_scale_log2(p->head_dim);
+  a.alpha = p->alpha;
+  a.sink = p->attention_sink;
+  a.window = p->window_size;
+  a.last_n = p->last_n_block;
+  a.native = p->native_normalize;
+  a.min_budget = p->min_budget;
+  return a;
+}
+
+int run_search(const fp_problem* p, const fp_ws_layout& L, void* ws, float* dp, float* dm,
+               const float* in_p, const float* in_m, hipStream_t s) {
+  fp::SearchArgs a = search_args(p, L, ws);
+  a.dump_p = dp;
+  a.dump_m = dm;
+  a.in_p = in_p;
+  a.in_m = in_m;
+  const bool from_scores = in_p != nullptr;
+  const hipError_t e = fp::launch_search(a, p->dtype, p->head_dim,
+                                         static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap,
+                                         from_scores, s);
+  return e == hipSuccess ? FP_OK : hip_fail(e, "search launch");
+}
+
+int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s) {
+  fp::AttnArgs a;
+  char* base = static_cast<char*>(ws);
+  a.tab = tables(L, ws);
+  a.q = static_cast<const uint16_t*>(p->q);
+  a.k = static_cast<const uint16_t*>(p->k);
+  a.v = static_cast<const uint16_t*>(p->v);
+  a.o = static_cast<uint16_t*>(p->o);
+  a.qst = p->q_stride_tok;
+  a.qhs = p->q_stride_head;
+  a.kst = p->k_stride_tok;
+  a.khs = p->k_stride_head;
+  a.vst = p->v_stride_tok;
+  a.vhs = p->v_stride_head;
+  a.ost = p->o_stride_tok;
+  a.ohs = p->o_stride_head;
+  a.idx = reinterpret_cast<const int32_t*>(base + L.idx_off);
+  a.cnt = reinterpret_cast<const int32_t*>(base + L.cnt_off);
+  a.tri_cap = L.tri_cap;
+  a.nb_sum_cap = L.nb_sum_cap;
+  a.B = p->batch;
+  a.Hq = p->num_q_heads;
+  a.Hkv = p->num_kv_heads;
+  a.sm_scale_log2 = sm_scale_log2(p->head_dim);
+  const hipError_t e = fp::launch_attn(a, p->dtype, p->head_dim,
+                                       static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap, s);
+  return e == hipSuccess ? FP_OK : hip_fail(e, "attention launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int fp_abi_version(void) { return 1; }
+
+const char* fp_last_error(void) { return g_last_error.c_str(); }
+
+int fp_workspace_layout(const fp_problem* p, fp_ws_layout* out) {
+  if (!out) return fail(FP_E_INVALID_ARG, "layout output is NULL");
+  return layout(p, out);
+}
+
+size_t fp_workspace_bytes(const fp_problem* p) {
+  fp_ws_layout L;
+  return layout(p, &L) == FP_OK ? L.total_bytes : 0;
+}
+
+int fp_plan(const fp_problem* p, void* ws, void* stream) {
+  fp_ws_layout L;
+  int rc = prepare(p, ws, &L);
+  if (rc != FP_OK) return rc;
+  return run_plan(p, L, ws, static_cast<hipStream_t>(stream));
+}
+
+int fp_pool_k(const fp_problem* p, void* ws, void* stream) {
+  fp_ws_layout L;
+  int rc = prepare(p, ws, &L);
+  if (rc != FP_OK) return rc;
+  return run_pool(p, L, ws, static_cast<hipStream_t>(stream));
+}
+
+int fp_search(const fp_problem* p, void* ws, float* dump_p, float* dump_m, void* stream) {
+  fp_ws_layout L;
+  int rc = prepare(p, ws, &L);
+  if (rc != FP_OK) return rc;
+  if ((dump_p == nullptr) != (dump_m == nullptr))
+    return fail(FP_E_INVALID_ARG, "dump_p and dump_m must both be set or both be NULL");
+  return run_search(p, L, ws, dump_p, dump_m, nullptr, nullptr, static_cast<hipStream_t>(stream));
+}
+
+int fp_select(const fp_problem* p, void* ws, const float* p_scores, const float* m_scores,
+              void* stream) {
+  fp_ws_layout L;
+  int rc = prepare(p, ws, &L);
+  if (rc != FP_OK) return rc;
+  if (!p_scores || !m_scores) return fail(FP_E_INVALID_ARG, "p_scores and m_scores must be non-NULL");
+  return run_search(p, L, ws, nullptr, nullptr, p_scores, m_scores,
+                    static_cast<hipStream_t>(stream));
+}
+
+int fp_sparse_attn_fwd(const fp_problem* p, void* ws, void* stream) {
+  fp_ws_layout L;
+  int rc = prepare(p, ws, &L);
+  if (rc != FP_OK) return rc;
+  return run_attn(p, L, ws, static_cast<hipStream_t>(stream));
+}
+
+int fp_flashprefill(const fp_problem* p, void* ws, void* stream) {
+  fp_ws_layout L;
+  int rc = prepare(p, ws, &L);
+  if (rc != FP_OK) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if ((rc = run_plan(p, L, ws, s)) != FP_OK) return rc;
+  if ((rc = run_pool(p, L, ws, s)) != FP_OK) return rc;
+  if ((rc = run_search(p, L, ws, nullptr, nullptr, nullptr, nullptr, s)) != FP_OK) return rc;
+  return run_attn(p, L, ws, s);
+}
+
+int fp_read_status(const fp_problem* p, void* ws, void* stream, uint32_t* status) {
+  fp_ws_layout L;
+  int rc = prepare(p, ws, &L);
+  if (rc != FP_OK) return rc;
+  if (!status) return fail(FP_E_INVALID_ARG, "status output is NULL");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = hipMemcpyAsync(status, static_cast<char*>(ws) + L.status_off, sizeof(uint32_t),
+                                hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  return e == hipSuccess ? FP_OK : hip_fail(e, "status read");
+}
+
+}  // extern "C"

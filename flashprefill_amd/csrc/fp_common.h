@@ -1,0 +1,148 @@
+// Device-side building blocks shared by the FlashPrefill gfx950 kernels:
+// element types, 16-byte vector moves, MFMA wrappers, wave/block reductions
+// and the workgroup -> work-item mapping.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "flashprefill.h"
+
+namespace fp {
+
+constexpr int kBlock = 128;       // tokens per block (block_size == k_stride)
+constexpr int kWave = 64;
+constexpr int kMaxBatch = 4096;   // sequences per call (plan kernel keeps them in LDS)
+constexpr int kMaxBlocks = 8192;  // blocks per sequence (1,048,576 tokens)
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// element types: 16-bit storage, fp32 math
+// ---------------------------------------------------------------------------
+struct BF16 {
+  typedef bf16x8 vec8;
+  static __device__ __forceinline__ float to_f32(uint16_t x) {
+    return __uint_as_float(static_cast<uint32_t>(x) << 16);
+  }
+  static __device__ __forceinline__ uint16_t from_f32(float f) {
+    __bf16 b = static_cast<__bf16>(f);  // v_cvt_pk_bf16_f32: round to nearest even
+    return __builtin_bit_cast(uint16_t, b);
+  }
+  static __device__ __forceinline__ f32x16 mfma32(vec8 a, vec8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+struct F16 {
+  typedef f16x8 vec8;
+  static __device__ __forceinline__ float to_f32(uint16_t x) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, x));
+  }
+  static __device__ __forceinline__ uint16_t from_f32(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  }
+  static __device__ __forceinline__ f32x16 mfma32(vec8 a, vec8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <typename T>
+__device__ __forceinline__ typename T::vec8 as_vec8(uint4 x) {
+  return __builtin_bit_cast(typename T::vec8, x);
+}
+
+__device__ __forceinline__ uint4 zero4() { return make_uint4(0u, 0u, 0u, 0u); }
+
+// 16-byte global load / store (address must be 16-byte aligned)
+__device__ __forceinline__ uint4 ld16(const void* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+__device__ __forceinline__ void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
+
+// ---------------------------------------------------------------------------
+// wave / block reductions (wave64)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float xor32_f(float x) { return __shfl_xor(x, 32); }
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ __forceinline__ double wave_sum_d(double x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+__device__ __forceinline__ int64_t wave_sum_i64(int64_t x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+// Block-wide max over blockDim.x threads; `red` needs blockDim.x/64 floats.
+__device__ __forceinline__ float block_max(float x, float* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  x = wave_max(x);
+  if (lane == 0) red[w] = x;
+  __syncthreads();
+  float r = red[0];
+  for (int k = 1; k < nw; ++k) r = fmaxf(r, red[k]);
+  __syncthreads();
+  return r;
+}
+
+// Block-wide fp64 sum; `red` needs blockDim.x/64 doubles.
+__device__ __forceinline__ double block_sum_d(double x, double* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  x = wave_sum_d(x);
+  if (lane == 0) red[w] = x;
+  __syncthreads();
+  double r = 0.0;
+  for (int k = 0; k < nw; ++k) r += red[k];
+  __syncthreads();
+  return r;
+}
+
+// Number of set bits of `mask` below this lane.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
+}
+
+// ---------------------------------------------------------------------------
+// Work items: (sequence b, q-block i) pairs ordered heaviest first by the plan
+// kernel, crossed with query heads. When Hq is a multiple of 8, the eight
+// XCDs (workgroups are dispatched round-robin, XCD = id % 8) each get Hq/8
+// consecutive heads, i.e. whole GQA groups when Hq/Hkv divides Hq/8, so K/V
+// blocks are re-read from the XCD's own L2; each XCD walks its items
+// heaviest first.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void map_item(int w, int num_q_heads, int& item, int& head) {
+  if ((num_q_heads & 7) == 0) {
+    const int x = w & 7, s = w >> 3, hpx = num_q_heads >> 3;
+    head = x * hpx + s % hpx;
+    item = s / hpx;
+  } else {
+    head = w % num_q_heads;
+    item = w / num_q_heads;
+  }
+}
+
+// Workspace views shared by all kernels (device pointers into the workspace).
+struct SeqTables {
+  uint32_t* status;
+  int64_t* seq_tile;   // [B+1] prefix of NB_b
+  int64_t* seq_tri;    // [B+1] prefix of NB_b (NB_b + 1) / 2
+  int64_t* seq_start;  // [B]   first token of sequence b
+  int32_t* seq_len;    // [B]   tokens of sequence b (0 when skipped)
+  int32_t* items;      // [2 * nb_sum_cap] (b, i) heaviest first
+};
+
+}  // namespace fp

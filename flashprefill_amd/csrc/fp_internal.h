@@ -1,0 +1,69 @@
+// Kernel argument blocks and launchers shared between the kernel files and the
+// C ABI (fp_capi.hip). Pointers are device pointers into the caller's tensors
+// or workspace; strides are in elements.
+#pragma once
+
+#include "fp_common.h"
+
+namespace fp {
+
+struct PlanArgs {
+  SeqTables tab;
+  const int32_t* cu;  // nullable: uniform batch
+  int32_t B;
+  int32_t uniform_len;
+  int32_t max_seq_len;
+  int32_t nb_max;
+  int64_t total_tokens;
+};
+
+struct PoolArgs {
+  SeqTables tab;
+  const uint16_t* k;
+  int64_t kst, khs;
+  uint16_t* mk;  // (sum NB, Hkv, D)
+  int32_t B;
+  int32_t Hkv;
+};
+
+struct SearchArgs {
+  SeqTables tab;
+  const uint16_t* q;
+  int64_t qst, qhs;
+  const uint16_t* mk;
+  int32_t* idx;
+  int32_t* cnt;
+  int64_t tri_cap;
+  int64_t nb_sum_cap;
+  const float* in_p;  // select-only mode: caller's block scores
+  const float* in_m;
+  float* dump_p;      // nullable
+  float* dump_m;
+  int32_t B, Hq, Hkv, nb_max;
+  float sm_scale_log2;  // fp32(fp32(1/sqrt(d)) * fp32(log2 e))
+  float alpha;
+  int32_t sink, window, last_n, native, min_budget;
+};
+
+struct AttnArgs {
+  SeqTables tab;
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  int64_t qst, qhs, kst, khs, vst, vhs, ost, ohs;
+  const int32_t* idx;
+  const int32_t* cnt;
+  int64_t tri_cap;
+  int64_t nb_sum_cap;
+  int32_t B, Hq, Hkv;
+  float sm_scale_log2;
+};
+
+hipError_t launch_plan(const PlanArgs& a, hipStream_t s);
+hipError_t launch_pool(const PoolArgs& a, int dtype, int head_dim, int64_t grid, hipStream_t s);
+hipError_t launch_search(const SearchArgs& a, int dtype, int head_dim, int64_t grid,
+                         bool from_scores, hipStream_t s);
+hipError_t launch_attn(const AttnArgs& a, int dtype, int head_dim, int64_t grid, hipStream_t s);
+
+}  // namespace fp

@@ -1,0 +1,232 @@
+// Sequence planning and K-block pooling for the FlashPrefill gfx950 path.
+//
+//   k_plan  — one workgroup turns cu_seqlens into per-sequence tables (block
+//             counts, block / triangle prefix sums) and the heaviest-first
+//             work-item list; replaces get_cu_tile_seqlens
+//             (ops/flashprefill_varlen_func.py:8-18) with no host sync.
+//   k_pool  — mean of every 128-token K block over its valid rows
+//             (ops/flashprefill_native_forward.py:21-67,
+//              ops/flashprefill_varlen_func.py:35-85). HBM-bound: each K byte
+//             is read once with 16-byte loads, sums are kept in fp32 and the
+//             mean is rounded once to the input dtype.
+#include "fp_internal.h"
+
+namespace fp {
+
+// Block-wide exclusive scan of one int64 per thread (blockDim.x <= 1024).
+__device__ int64_t block_exscan_i64(int64_t v, int64_t* red, int64_t* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  int64_t x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) red[w] = x;
+  __syncthreads();
+  if (w == 0) {
+    int64_t r = lane < nw ? red[lane] : 0;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int64_t y = __shfl_up(r, o);
+      if (lane >= o) r += y;
+    }
+    if (lane < nw) red[lane] = r;
+  }
+  __syncthreads();
+  const int64_t wave_off = w > 0 ? red[w - 1] : 0;
+  *total = red[nw - 1];
+  __syncthreads();
+  return wave_off + x - v;
+}
+
+__global__ __launch_bounds__(1024) void k_plan(PlanArgs a) {
+  __shared__ int32_t s_pre[kMaxBatch + 1];  // NB prefix over sequences
+  __shared__ int32_t s_lvl[kMaxBlocks];     // per q-block level: counts, then cursors
+  __shared__ int64_t s_red[16];
+  __shared__ uint32_t s_status;
+  const int t = threadIdx.x, nt = blockDim.x;
+  const SeqTables& tab = a.tab;
+  if (t == 0) s_status = 0u;
+  __syncthreads();
+
+  // 1. per-sequence lengths and validity
+  for (int b = t; b < a.B; b += nt) {
+    int64_t start, end;
+    if (a.cu) {
+      start = a.cu[b];
+      end = a.cu[b + 1];
+    } else {
+      start = static_cast<int64_t>(b) * a.uniform_len;
+      end = start + a.uniform_len;
+    }
+    int64_t len = end - start;
+    if (start < 0 || len < 0 || end > a.total_tokens) {
+      atomicOr(&s_status, FP_STATUS_BAD_CU_SEQLENS);
+      len = 0;
+      start = 0;
+    } else if (len > a.max_seq_len) {
+      atomicOr(&s_status, FP_STATUS_SEQ_TOO_LONG);
+      len = 0;
+    }
+    tab.seq_start[b] = start;
+    tab.seq_len[b] = static_cast<int32_t>(len);
+    s_pre[b] = static_cast<int32_t>((len + kBlock - 1) / kBlock);
+  }
+  for (int i = t; i < a.nb_max; i += nt) s_lvl[i] = 0;
+  __syncthreads();
+
+  // 2. prefix sums of NB_b and NB_b (NB_b + 1) / 2; level histogram
+  int64_t carry_tile = 0, carry_tri = 0;
+  for (int base = 0; base < a.B; base += nt) {
+    const int b = base + t;
+    const int64_t nb = b < a.B ? s_pre[b] : 0;
+    int64_t tot1, tot2;
+    const int64_t e1 = block_exscan_i64(nb, s_red, &tot1);
+    const int64_t e2 = block_exscan_i64(nb * (nb + 1) / 2, s_red, &tot2);
+    if (b < a.B) {
+      tab.seq_tile[b] = carry_tile + e1;
+      tab.seq_tri[b] = carry_tri + e2;
+      if (nb > 0) atomicAdd(&s_lvl[nb - 1], 1);
+    }
+    __syncthreads();  // all reads of s_pre[b] in this chunk are done
+    if (b < a.B) s_pre[b] = static_cast<int32_t>(carry_tile + e1);
+    carry_tile += tot1;
+    carry_tri += tot2;
+  }
+  if (t == 0) {
+    tab.seq_tile[a.B] = carry_tile;
+    tab.seq_tri[a.B] = carry_tri;
+    s_pre[a.B] = static_cast<int32_t>(carry_tile);
+  }
+  __syncthreads();
+
+  // 3. level sizes c_i = #{b : NB_b > i} (suffix sum of the histogram), then
+  //    level offsets in heaviest-first order (exclusive suffix sum of c_i).
+  for (int pass = 0; pass < 2; ++pass) {
+    int64_t carry = 0;
+    for (int base = 0; base < a.nb_max; base += nt) {
+      const int i = a.nb_max - 1 - (base + t);  // descending level
+      const int64_t v = i >= 0 ? s_lvl[i] : 0;
+      int64_t tot;
+      const int64_t ex = block_exscan_i64(v, s_red, &tot);
+      if (i >= 0) s_lvl[i] = static_cast<int32_t>(carry + (pass == 0 ? ex + v : ex));
+      carry += tot;
+      __syncthreads();
+    }
+  }
+
+  // 4. scatter (b, i) items: position = level offset + arrival order
+  const int nsum = s_pre[a.B];
+  for (int g = t; g < nsum; g += nt) {
+    int lo = 0, hi = a.B - 1;  // last b with s_pre[b] <= g
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_pre[mid] <= g) lo = mid; else hi = mid - 1;
+    }
+    const int i = g - s_pre[lo];
+    const int pos = atomicAdd(&s_lvl[i], 1);
+    tab.items[2 * pos] = lo;
+    tab.items[2 * pos + 1] = i;
+  }
+  __syncthreads();
+  if (t == 0) *tab.status = s_status;
+}
+
+// Sequence owning global block g (binary search over seq_tile).
+__device__ __forceinline__ int find_seq(const int64_t* seq_tile, int B, int64_t g) {
+  int lo = 0, hi = B - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (seq_tile[mid] <= g) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void k_pool(PoolArgs a) {
+  __shared__ float red[256 * 8];
+  const int64_t g = blockIdx.x;
+  const int64_t nsum = a.tab.seq_tile[a.B];
+  if (g >= nsum) return;
+  const int b = find_seq(a.tab.seq_tile, a.B, g);
+  const int i = static_cast<int>(g - a.tab.seq_tile[b]);
+  const int L = a.tab.seq_len[b];
+  const int64_t t0 = a.tab.seq_start[b] + static_cast<int64_t>(i) * kBlock;
+  const int rows = min(kBlock, L - i * kBlock);
+  constexpr int CPH = D / 8;                 // 16-byte chunks per head row
+  const int C = a.Hkv * CPH;                 // chunks per token row (all kv heads)
+  const int t = threadIdx.x;
+  const float inv = 1.0f / static_cast<float>(rows);
+  uint16_t* out = a.mk + g * static_cast<int64_t>(a.Hkv) * D;
+
+  if (C <= 256) {
+    const int R = 256 / C;  // row groups reduced through LDS
+    const int c = t % C, rg = t / C;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (rg < R) {
+      const int hh = c / CPH, x0 = (c % CPH) * 8;
+      const uint16_t* src = a.k + t0 * a.kst + hh * a.khs + x0;
+      for (int r = rg; r < rows; r += R) {
+        const uint4 v = ld16(src + static_cast<int64_t>(r) * a.kst);
+        const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[q] += T::to_f32(e[q]);
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) red[(rg * C + c) * 8 + q] = acc[q];
+    }
+    __syncthreads();
+    if (rg == 0) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        float s = 0.f;
+        for (int r = 0; r < R; ++r) s += red[(r * C + c) * 8 + q];
+        acc[q] = s;
+      }
+      uint16_t o[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) o[q] = T::from_f32(acc[q] * inv);
+      st16(out + c * 8, *reinterpret_cast<const uint4*>(o));
+    }
+  } else {
+    for (int c = t; c < C; c += 256) {
+      const int hh = c / CPH, x0 = (c % CPH) * 8;
+      const uint16_t* src = a.k + t0 * a.kst + hh * a.khs + x0;
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      for (int r = 0; r < rows; ++r) {
+        const uint4 v = ld16(src + static_cast<int64_t>(r) * a.kst);
+        const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[q] += T::to_f32(e[q]);
+      }
+      uint16_t o[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) o[q] = T::from_f32(acc[q] * inv);
+      st16(out + c * 8, *reinterpret_cast<const uint4*>(o));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+hipError_t launch_plan(const PlanArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(k_plan, dim3(1), dim3(1024), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_pool(const PoolArgs& a, int dtype, int head_dim, int64_t grid, hipStream_t s) {
+  if (grid <= 0) return hipSuccess;
+  const dim3 g(static_cast<unsigned>(grid)), blk(256);
+  if (dtype == FP_DTYPE_BF16) {
+    if (head_dim == 128) hipLaunchKernelGGL((k_pool<BF16, 128>), g, blk, 0, s, a);
+    else hipLaunchKernelGGL((k_pool<BF16, 64>), g, blk, 0, s, a);
+  } else {
+    if (head_dim == 128) hipLaunchKernelGGL((k_pool<F16, 128>), g, blk, 0, s, a);
+    else hipLaunchKernelGGL((k_pool<F16, 64>), g, blk, 0, s, a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace fp

@@ -1,0 +1,225 @@
+// Fused block scoring + pattern selection for the FlashPrefill gfx950 path.
+//
+// One workgroup (4 waves) owns one (query head h, sequence b, q-block i) row:
+//
+//  1. score (ops/flashprefill_native_forward.py:87-188,
+//     ops/flashprefill_varlen_func.py:106-217): the 128 full-resolution query
+//     rows of block i against every pooled key j <= i on bf16/fp16 MFMA
+//     (v_mfma_f32_32x32x16), S = Q . mk^T. Each wave keeps the whole 128 x d Q
+//     block in registers as A operands and walks its own 32-column tiles of
+//     pooled keys, so the per-column reductions over the 128 rows
+//     (m_ij = max_r s_r, p_ij = sum_r exp2(s_r - m_ij)) are in-register plus
+//     one cross-half exchange; nothing is shared between waves. The causal
+//     block rule keeps all rows for j < i and only row 127 for j == i (:157).
+//     (p, m) of the row stay in LDS (optionally dumped to global for parity
+//     tests).
+//  2. select (ops/flashprefill_native_forward.py:347-403,
+//     ops/flashprefill_varlen_func.py:240-409,656): M = max_j m_ij,
+//     S_ij = p_ij * exp2(m_ij - M) [native: / (sum_j S_ij + 1e-9)],
+//     keep j if S_ij >= alpha * max_j S_ij, or j < sink, or 0 <= i-j < window,
+//     or i >= NB - last_n. No sort, no prefix pass over global memory: the
+//     kept j are compacted in ascending order with wave ballots.
+//
+// Selection arithmetic is made order independent so that the same fp32 (p, m)
+// always yields the same index set: exp2 is evaluated in fp64 and rounded
+// once to fp32 (correctly rounded fp32 exp2), and the native row sum is
+// accumulated in fp64 and rounded once.
+#include "fp_internal.h"
+
+namespace fp {
+
+__device__ __forceinline__ float exp2_rn(float x) {
+  return static_cast<float>(exp2(static_cast<double>(x)));
+}
+
+// Select over p (pl) and m (ml) of one row held in LDS; writes the ascending
+// index list and its length. Uses 256 threads.
+__device__ void select_row(float* pl, const float* ml, int n, int i, int nb,
+                           const SearchArgs& a, int32_t* list, int32_t* count) {
+#pragma clang fp contract(off)
+  __shared__ float redf[4];
+  __shared__ double redd[4];
+  __shared__ int wtot[4];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+
+  float lm = -INFINITY;
+  for (int j = t; j < n; j += 256) lm = fmaxf(lm, ml[j]);
+  const float M = block_max(lm, redf);
+
+  double ls = 0.0;
+  for (int j = t; j < n; j += 256) {
+    const float s = pl[j] * exp2_rn(ml[j] - M);
+    pl[j] = s;
+    ls += static_cast<double>(s);
+  }
+  if (a.native) {
+    const float tot = static_cast<float>(block_sum_d(ls, redd));
+    const float denom = tot + 1e-9f;
+    for (int j = t; j < n; j += 256) pl[j] = pl[j] / denom;
+  }
+  float lmax = 0.0f;
+  for (int j = t; j < n; j += 256) lmax = fmaxf(lmax, pl[j]);
+  const float maxS = block_max(lmax, redf);
+  const float thr = maxS * a.alpha;
+  const bool last_rows = i >= nb - a.last_n;
+
+  int running = 0;
+  for (int base = 0; base < n; base += 256) {
+    const int j = base + t;
+    bool keep = false;
+    if (j < n) {
+      keep = (pl[j] >= thr) || (j < a.sink) || (i - j < a.window) || last_rows;
+    }
+    const uint64_t bal = __ballot(keep);
+    if (lane == 0) wtot[w] = __popcll(bal);
+    __syncthreads();
+    int off = running;
+    for (int k = 0; k < w; ++k) off += wtot[k];
+    if (keep) list[off + lanes_below(bal)] = j;
+    running += wtot[0] + wtot[1] + wtot[2] + wtot[3];
+    __syncthreads();
+  }
+  if (t == 0) *count = running;
+}
+
+template <typename T, int D, bool FROM_SCORES>
+__global__ __launch_bounds__(256, 2) void k_search(SearchArgs a) {
+  extern __shared__ float dyn[];
+  float* pl = dyn;
+  float* ml = dyn + a.nb_max;
+  int item, h;
+  map_item(blockIdx.x, a.Hq, item, h);
+  const int64_t nitems = a.tab.seq_tile[a.B];
+  if (item >= nitems) return;
+  const int b = a.tab.items[2 * item];
+  const int i = a.tab.items[2 * item + 1];
+  const int64_t tile_b = a.tab.seq_tile[b];
+  const int nb = static_cast<int>(a.tab.seq_tile[b + 1] - tile_b);
+  const int L = a.tab.seq_len[b];
+  const int64_t t0 = a.tab.seq_start[b];
+  const int n = i + 1;
+  const int64_t row_tri = static_cast<int64_t>(h) * a.tri_cap + a.tab.seq_tri[b] +
+                          static_cast<int64_t>(i) * (i + 1) / 2;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+
+  if constexpr (FROM_SCORES) {
+    for (int j = t; j < n; j += 256) {
+      pl[j] = a.in_p[row_tri + j];
+      ml[j] = a.in_m[row_tri + j];
+    }
+  } else {
+    constexpr int KS = D / 16;  // MFMA k-steps over the head dim
+    const int kvh = h / (a.Hq / a.Hkv);
+    const int half = lane >> 5, l32 = lane & 31;
+    const float c = a.sm_scale_log2;
+    // Q block as MFMA A operands: rows 32*rg + l32, dims 16*s + 8*half .. +7
+    typename T::vec8 qa[4][KS];
+#pragma unroll
+    for (int rg = 0; rg < 4; ++rg) {
+      const int row = 32 * rg + l32;
+      const bool valid = i * kBlock + row < L;
+      const uint16_t* qp = a.q + (t0 + static_cast<int64_t>(i) * kBlock + row) * a.qst +
+                           static_cast<int64_t>(h) * a.qhs + 8 * half;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) qa[rg][s] = as_vec8<T>(valid ? ld16(qp + 16 * s) : zero4());
+    }
+    const int64_t mk_row = static_cast<int64_t>(a.Hkv) * D;
+    const uint16_t* mkb = a.mk + tile_b * mk_row + static_cast<int64_t>(kvh) * D + 8 * half;
+    const int ntiles = (n + 31) >> 5;
+    for (int tile = w; tile < ntiles; tile += 4) {
+      const int j = 32 * tile + l32;
+      const bool jv = j < n;
+      typename T::vec8 kb[KS];
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        kb[s] = as_vec8<T>(jv ? ld16(mkb + static_cast<int64_t>(j) * mk_row + 16 * s) : zero4());
+      f32x16 acc[4];
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg) acc[rg] = f32x16{};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg) acc[rg] = T::mfma32(qa[rg][s], kb[s], acc[rg]);
+
+      // acc[rg][v] = Q[32 rg + 8 (v/4) + 4 half + v%4] . mk[j]
+      float mx = -INFINITY, sum = 0.0f, m;
+      if (tile + 1 < ntiles) {  // every column j < i: all 128 rows count
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc[rg][v]);
+        mx = fmaxf(mx, xor32_f(mx));
+        m = mx * c;
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) sum += __builtin_amdgcn_exp2f(fmaf(acc[rg][v], c, -m));
+      } else {  // last tile: j < i all rows, j == i row 127 only, j > i none
+        const bool full = j < i, diag = j == i;
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int row = 32 * rg + 8 * (v >> 2) + 4 * half + (v & 3);
+            if (full || (diag && row == kBlock - 1)) mx = fmaxf(mx, acc[rg][v]);
+          }
+        mx = fmaxf(mx, xor32_f(mx));
+        m = mx * c;
+#pragma unroll
+        for (int rg = 0; rg < 4; ++rg)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int row = 32 * rg + 8 * (v >> 2) + 4 * half + (v & 3);
+            if (full || (diag && row == kBlock - 1))
+              sum += __builtin_amdgcn_exp2f(fmaf(acc[rg][v], c, -m));
+          }
+      }
+      sum += xor32_f(sum);
+      if (half == 0 && jv) {
+        pl[j] = sum;
+        ml[j] = m;
+        if (a.dump_p) {
+          a.dump_p[row_tri + j] = sum;
+          a.dump_m[row_tri + j] = m;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  int32_t* list = a.idx + row_tri;
+  int32_t* count = a.cnt + static_cast<int64_t>(h) * a.nb_sum_cap + tile_b + i;
+  select_row(pl, ml, n, i, nb, a, list, count);
+}
+
+template <typename T, int D, bool FROM_SCORES>
+hipError_t launch_search_t(const SearchArgs& a, int64_t grid, hipStream_t s) {
+  const size_t shm = 2 * sizeof(float) * static_cast<size_t>(a.nb_max);
+  if (shm > 48 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_search<T, D, FROM_SCORES>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(shm));
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((k_search<T, D, FROM_SCORES>), dim3(static_cast<unsigned>(grid)), dim3(256),
+                     shm, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_search(const SearchArgs& a, int dtype, int head_dim, int64_t grid,
+                         bool from_scores, hipStream_t s) {
+  if (grid <= 0) return hipSuccess;
+  if (dtype == FP_DTYPE_BF16) {
+    if (head_dim == 128)
+      return from_scores ? launch_search_t<BF16, 128, true>(a, grid, s)
+                         : launch_search_t<BF16, 128, false>(a, grid, s);
+    return from_scores ? launch_search_t<BF16, 64, true>(a, grid, s)
+                       : launch_search_t<BF16, 64, false>(a, grid, s);
+  }
+  if (head_dim == 128)
+    return from_scores ? launch_search_t<F16, 128, true>(a, grid, s)
+                       : launch_search_t<F16, 128, false>(a, grid, s);
+  return from_scores ? launch_search_t<F16, 64, true>(a, grid, s)
+                     : launch_search_t<F16, 64, false>(a, grid, s);
+}
+
+}  // namespace fp

@@ -1,0 +1,66 @@
+"""Batched FlashPrefill operator: drop-in for ``flash_prefill``
+(``ops/flashprefill_native_forward.py:480-499``), the entry point of the HF
+model callers (``ruler/models/llama.py:303``, ``ruler/models/qwen2.py:149``,
+``ruler/models/qwen3.py:189``, ``patches/patch_qwen2_5_vl.py:58``,
+``patches/patch_qwen3_moe_vl.py:49``).
+
+Inputs are ``(B, S, H, d)`` (the code reads ``(b, s, h, d)``, :416, whatever
+its docstring says). The batch is run as B sequences of S tokens through the
+same kernels as the varlen entry point, with the native normalisation
+``S /= (sum_j S + 1e-9)`` (:401).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .runtime import FlashPrefillCall
+
+
+def _readable_in_place(t: torch.Tensor) -> bool:
+    """True when (B, S, H, d) packs along tokens with the head dim contiguous
+    and 16-byte aligned rows, so the kernels can use it without a copy."""
+    S = t.shape[1]
+    return (t.stride(-1) == 1 and t.stride(0) == S * t.stride(1)
+            and t.stride(1) % 8 == 0 and t.stride(2) % 8 == 0 and t.data_ptr() % 16 == 0)
+
+
+def _packed_view(t: torch.Tensor) -> torch.Tensor:
+    """(B, S, H, d) -> (B*S, H, d) view of ``t`` (or of a contiguous copy when
+    ``t`` cannot be read in place; the reference forces contiguity, :408)."""
+    B, S, H, d = t.shape
+    src = t if _readable_in_place(t) else t.contiguous()
+    return src.as_strided((B * S, H, d), (src.stride(1), src.stride(2), 1))
+
+
+@torch.no_grad()
+def flash_prefill(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    out: torch.Tensor,
+    block_size: int,
+    attention_sink: int,
+    window_size: int,
+    alpha: float,
+    last_n_block_full: int,
+    min_budget: int,
+) -> None:
+    """q (B, S, Hq, d), k/v (B, S, Hkv, d); ``out`` (B, S, Hq, d) written in place."""
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4 or out.dim() != 4:
+        raise ValueError("flash_prefill expects (batch, seq, heads, head_dim) tensors")
+    B, S, Hq, d = q.shape
+    if out.shape != q.shape:
+        raise ValueError(f"out shape {tuple(out.shape)} != q shape {tuple(q.shape)}")
+    q2, k2, v2 = _packed_view(q), _packed_view(k), _packed_view(v)
+    direct = _readable_in_place(out)
+    o2 = _packed_view(out) if direct else torch.empty(B * S, Hq, d, dtype=q.dtype,
+                                                       device=q.device)
+    call = FlashPrefillCall(q2, k2, v2, o2, None, max(S, 1), alpha=float(alpha),
+                            attention_sink=attention_sink, window_size=window_size,
+                            last_n_block=last_n_block_full, native_normalize=True,
+                            min_budget=min_budget, block_size=block_size, batch=B,
+                            uniform_seq_len=S)
+    call.run()
+    if not direct:
+        out.copy_(o2.view(B, S, Hq, d))

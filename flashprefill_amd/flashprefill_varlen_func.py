@@ -1,0 +1,60 @@
+"""Varlen FlashPrefill operator: drop-in for ``flash_prefill_varlen_func``
+(``ops/flashprefill_varlen_func.py:722-743``), the entry point the vLLM patch
+loaders call (``patches/patch_loader_vllm_0_12_0.py:187-199``,
+``patches/patch_loader_vllm_0_10_0.py:246-258``).
+
+Same arguments, defaults and in-place ``o`` semantics. The work runs on the
+current torch stream through the C ABI (``include/flashprefill.h``): plan ->
+pool K -> search (score + select) -> block-sparse attention, with no host
+synchronisation (the reference syncs three times, :680,:696,:716).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .runtime import FlashPrefillCall
+
+
+def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
+    """Return ``t`` itself when the kernels can read it in place (head dim
+    contiguous, 16-byte aligned rows), else a contiguous copy — the reference
+    forces contiguity for the same purpose (``fla.utils.contiguous``, :580)."""
+    ok = (t.stride(-1) == 1 and all(s % 8 == 0 for s in t.stride()[:-1])
+          and t.data_ptr() % 16 == 0)
+    return t if ok else t.contiguous()
+
+
+@torch.no_grad()
+def flash_prefill_varlen_func(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    o: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    max_seq_len: int,
+    alpha: float,
+    block_size: int = 128,
+    attention_sink: int = 2,
+    window_size: int = 4,
+    last_n_block: int = 2,
+) -> None:
+    """q (T, Hq, d), k/v (T, Hkv, d), o (T, Hq, d) written in place;
+    cu_seqlens int32 (B+1,) token offsets; max_seq_len >= every length.
+
+    Raises ValueError for malformed arguments and NotImplementedError for
+    arguments the reference accepts but this build does not (fp32 inputs,
+    head_dim other than 64/128, block_size other than 128).
+    """
+    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    target = o
+    if not (o.stride(-1) == 1 and all(s % 8 == 0 for s in o.stride()[:-1])
+            and o.data_ptr() % 16 == 0):
+        o = torch.empty_like(q)
+    call = FlashPrefillCall(q, k, v, o, cu_seqlens, int(max_seq_len), alpha=float(alpha),
+                            attention_sink=attention_sink, window_size=window_size,
+                            last_n_block=last_n_block, native_normalize=False,
+                            block_size=block_size)
+    call.run()
+    if o is not target:
+        target.copy_(o)

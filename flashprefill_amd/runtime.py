@@ -1,0 +1,230 @@
+"""Host-side driver of the C ABI: builds the ``fp_problem`` descriptor from
+torch tensors, owns the workspace (from torch's caching allocator, so it is
+stream ordered), launches on torch's current stream, and exposes the
+workspace intermediates (pooled K, per-row index lists and counts) as tensor
+views for parity checks.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import List, Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.bfloat16: _lib.FP_DTYPE_BF16, torch.float16: _lib.FP_DTYPE_F16}
+BLOCK = 128
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype not in _DTYPES:
+        raise NotImplementedError(
+            f"FlashPrefill GPU path supports bfloat16 and float16 inputs, got {t.dtype}")
+    return _DTYPES[t.dtype]
+
+
+class FlashPrefillCall:
+    """One operator invocation on packed (T, H, d) tensors.
+
+    ``cu_seqlens`` is a device int32 tensor of B+1 offsets, or None for
+    ``batch`` sequences of ``uniform_seq_len`` tokens (the batched layout).
+    """
+
+    def __init__(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+                 cu_seqlens: Optional[torch.Tensor], max_seq_len: int, *, alpha: float,
+                 attention_sink: int = 2, window_size: int = 4, last_n_block: int = 2,
+                 native_normalize: bool = False, min_budget: int = 0,
+                 block_size: int = BLOCK, batch: Optional[int] = None,
+                 uniform_seq_len: int = 0, workspace: Optional[torch.Tensor] = None):
+        for name, t in (("q", q), ("k", k), ("v", v), ("o", o)):
+            if t.dim() != 3:
+                raise ValueError(f"{name} must be (tokens, heads, head_dim), got {tuple(t.shape)}")
+            if not t.is_cuda:
+                raise ValueError(f"{name} must be a GPU tensor")
+            if t.stride(-1) != 1:
+                raise ValueError(f"{name} must have a contiguous head dimension")
+        if not (q.dtype == k.dtype == v.dtype == o.dtype):
+            raise ValueError("q, k, v and o must share one dtype")
+        T, Hq, d = q.shape
+        Hkv = k.shape[1]
+        if k.shape != v.shape or k.shape[0] != T or k.shape[2] != d or o.shape != q.shape:
+            raise ValueError(f"shape mismatch: q{tuple(q.shape)} k{tuple(k.shape)} "
+                             f"v{tuple(v.shape)} o{tuple(o.shape)}")
+        self.device = q.device
+        self.tensors = (q, k, v, o)
+        if cu_seqlens is not None:
+            cu_seqlens = cu_seqlens.to(device=self.device, dtype=torch.int32).contiguous()
+            batch = cu_seqlens.numel() - 1
+        self.cu_seqlens = cu_seqlens
+        self.batch = int(batch)
+        self.max_seq_len = int(max_seq_len)
+        self.Hq, self.Hkv, self.d = Hq, Hkv, d
+        P = _lib.FpProblem()
+        P.q, P.k, P.v, P.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
+        P.q_stride_tok, P.q_stride_head = q.stride(0), q.stride(1)
+        P.k_stride_tok, P.k_stride_head = k.stride(0), k.stride(1)
+        P.v_stride_tok, P.v_stride_head = v.stride(0), v.stride(1)
+        P.o_stride_tok, P.o_stride_head = o.stride(0), o.stride(1)
+        P.cu_seqlens = cu_seqlens.data_ptr() if cu_seqlens is not None else None
+        P.batch = self.batch
+        P.uniform_seq_len = int(uniform_seq_len)
+        P.max_seq_len = self.max_seq_len
+        P.total_tokens = T
+        P.num_q_heads, P.num_kv_heads, P.head_dim = Hq, Hkv, d
+        P.dtype = _dtype_code(q)
+        P.block_size = int(block_size)
+        P.alpha = float(alpha)
+        P.attention_sink = int(attention_sink)
+        P.window_size = int(window_size)
+        P.last_n_block = int(last_n_block)
+        P.native_normalize = 1 if native_normalize else 0
+        P.min_budget = int(min_budget)
+        self.P = P
+        self.lib = _lib.load()
+        L = _lib.FpWsLayout()
+        _lib.check(self.lib.fp_workspace_layout(ctypes.byref(P), ctypes.byref(L)))
+        self.layout = L
+        if workspace is None or workspace.numel() < L.total_bytes:
+            workspace = torch.empty(L.total_bytes, dtype=torch.uint8, device=self.device)
+        self.workspace = workspace
+
+    # -- launches ---------------------------------------------------------
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def _ws(self) -> int:
+        return self.workspace.data_ptr()
+
+    def run(self) -> None:
+        _lib.check(self.lib.fp_flashprefill(ctypes.byref(self.P), self._ws(), self._stream()))
+
+    def plan(self) -> None:
+        _lib.check(self.lib.fp_plan(ctypes.byref(self.P), self._ws(), self._stream()))
+
+    def pool(self) -> None:
+        _lib.check(self.lib.fp_pool_k(ctypes.byref(self.P), self._ws(), self._stream()))
+
+    def search(self, dump: bool = False) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
+        dp = dm = None
+        if dump:
+            n = self.Hq * self.layout.tri_cap
+            dp = torch.full((n,), float("nan"), dtype=torch.float32, device=self.device)
+            dm = torch.full((n,), float("nan"), dtype=torch.float32, device=self.device)
+        _lib.check(self.lib.fp_search(ctypes.byref(self.P), self._ws(),
+                                      dp.data_ptr() if dump else None,
+                                      dm.data_ptr() if dump else None, self._stream()))
+        return (dp, dm) if dump else None
+
+    def select(self, p_tri: torch.Tensor, m_tri: torch.Tensor) -> None:
+        for t in (p_tri, m_tri):
+            if t.dtype != torch.float32 or not t.is_contiguous() or \
+                    t.numel() < self.Hq * self.layout.tri_cap or t.device != self.device:
+                raise ValueError("scores must be contiguous fp32 device tensors of Hq*tri_cap entries")
+        _lib.check(self.lib.fp_select(ctypes.byref(self.P), self._ws(), p_tri.data_ptr(),
+                                      m_tri.data_ptr(), self._stream()))
+
+    def attn(self) -> None:
+        _lib.check(self.lib.fp_sparse_attn_fwd(ctypes.byref(self.P), self._ws(), self._stream()))
+
+    def status(self) -> int:
+        st = ctypes.c_uint32(0)
+        _lib.check(self.lib.fp_read_status(ctypes.byref(self.P), self._ws(), self._stream(),
+                                           ctypes.byref(st)))
+        return int(st.value)
+
+    # -- workspace views (valid after the stages that write them) ----------
+    def _view(self, off: int, dtype: torch.dtype, n: int) -> torch.Tensor:
+        nbytes = n * torch.empty((), dtype=dtype).element_size()
+        return self.workspace[off:off + nbytes].view(dtype)
+
+    def seq_tables(self) -> Tuple[List[int], List[int], List[int], List[int]]:
+        L, B = self.layout, self.batch
+        tile = self._view(L.seq_tile_off, torch.int64, B + 1).tolist()
+        tri = self._view(L.seq_tri_off, torch.int64, B + 1).tolist()
+        start = self._view(L.seq_start_off, torch.int64, B).tolist()
+        ln = self._view(L.seq_len_off, torch.int32, B).tolist()
+        return tile, tri, start, ln
+
+    def items(self) -> torch.Tensor:
+        tile, _, _, _ = self.seq_tables()
+        return self._view(self.layout.items_off, torch.int32, 2 * tile[-1]).view(-1, 2)
+
+    def pooled_k(self) -> torch.Tensor:
+        tile, _, _, _ = self.seq_tables()
+        n = tile[-1] * self.Hkv * self.d
+        return self._view(self.layout.mk_off, self.tensors[0].dtype, n).view(tile[-1], self.Hkv,
+                                                                              self.d)
+
+    def counts(self) -> torch.Tensor:
+        L = self.layout
+        return self._view(L.cnt_off, torch.int32, self.Hq * L.nb_sum_cap).view(self.Hq,
+                                                                               L.nb_sum_cap)
+
+    def index_lists(self) -> torch.Tensor:
+        L = self.layout
+        return self._view(L.idx_off, torch.int32, self.Hq * L.tri_cap).view(self.Hq, L.tri_cap)
+
+    def selection_masks(self) -> List[torch.Tensor]:
+        """Per-sequence (Hq, NB, NB) bool masks rebuilt from the index lists (CPU)."""
+        tile, tri, _, _ = self.seq_tables()
+        cnt = self.counts().cpu()
+        idx = self.index_lists().cpu()
+        out = []
+        for b in range(self.batch):
+            nb = tile[b + 1] - tile[b]
+            mask = torch.zeros(self.Hq, nb, nb, dtype=torch.bool)
+            for i in range(nb):
+                base = tri[b] + i * (i + 1) // 2
+                for h in range(self.Hq):
+                    c = int(cnt[h, tile[b] + i])
+                    if c:
+                        mask[h, i, idx[h, base:base + c].long()] = True
+            out.append(mask)
+        return out
+
+    def ordered_lists_ok(self) -> bool:
+        """True when every row's list is strictly ascending (CPU check)."""
+        tile, tri, _, _ = self.seq_tables()
+        cnt = self.counts().cpu()
+        idx = self.index_lists().cpu()
+        for b in range(self.batch):
+            nb = tile[b + 1] - tile[b]
+            for i in range(nb):
+                base = tri[b] + i * (i + 1) // 2
+                for h in range(self.Hq):
+                    c = int(cnt[h, tile[b] + i])
+                    row = idx[h, base:base + c]
+                    if c > 1 and not bool((row[1:] > row[:-1]).all()):
+                        return False
+        return True
+
+    def tri_scores(self, scores: Sequence[torch.Tensor]) -> torch.Tensor:
+        """Pack per-sequence (Hq, NB, NB) fp32 arrays into the triangular
+        (Hq * tri_cap) device layout that fp_select reads."""
+        tile, tri, _, _ = self.seq_tables()
+        L = self.layout
+        out = torch.zeros(self.Hq, L.tri_cap, dtype=torch.float32)
+        for b, s in enumerate(scores):
+            nb = tile[b + 1] - tile[b]
+            r, c = torch.tril_indices(nb, nb)
+            pos = tri[b] + r * (r + 1) // 2 + c
+            out[:, pos] = s[:, r, c].float()
+        return out.reshape(-1).to(self.device)
+
+    def untri_scores(self, flat: torch.Tensor) -> List[torch.Tensor]:
+        """Inverse of tri_scores: device triangular dump -> per-sequence
+        (Hq, NB, NB) CPU arrays (upper triangle = NaN)."""
+        tile, tri, _, _ = self.seq_tables()
+        L = self.layout
+        flat = flat.view(self.Hq, L.tri_cap).cpu()
+        out = []
+        for b in range(self.batch):
+            nb = tile[b + 1] - tile[b]
+            r, c = torch.tril_indices(nb, nb)
+            pos = tri[b] + r * (r + 1) // 2 + c
+            full = torch.full((self.Hq, nb, nb), float("nan"))
+            full[:, r, c] = flat[:, pos]
+            out.append(full)
+        return out

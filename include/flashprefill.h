@@ -1,0 +1,145 @@
+/*
+ * flashprefill.h — C ABI of the MI355X (gfx950) FlashPrefill sparse-prefill
+ * attention path.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes in
+ * an `fp_problem` descriptor, a caller-owned device workspace of
+ * `fp_workspace_bytes()` bytes, and the HIP stream to launch on (passed as
+ * `void*` so that no HIP header is needed to bind this ABI). Nothing here
+ * allocates device memory, synchronises the host, or keeps state between
+ * calls; calls on different streams with different workspaces may overlap.
+ *
+ * Return value: FP_OK (0) or a negative FP_E* code; `fp_last_error()` gives a
+ * human-readable message for the last failure on the calling thread.
+ *
+ * Reference interfaces replaced (qhfan/FlashPrefill, all Python/Triton):
+ *   fp_flashprefill        flash_prefill_varlen_func   ops/flashprefill_varlen_func.py:722-743
+ *                          flash_prefill               ops/flashprefill_native_forward.py:480-499
+ *                          (FlashPrefill_varlen.forward :577-720, FlashPrefill.forward :405-476)
+ *   fp_plan                get_cu_tile_seqlens         ops/flashprefill_varlen_func.py:8-18
+ *   fp_pool_k              compute_mean_vector(_varlen) ops/flashprefill_native_forward.py:21-67,
+ *                                                      ops/flashprefill_varlen_func.py:35-85
+ *   fp_search              compute_block_score(_varlen) + normalize_scores / compute_block_sub_max_varlen
+ *                          + deal_output_score / compute_block_max_varlen + index compaction
+ *                          ops/flashprefill_native_forward.py:87-188,347-403,452-454
+ *                          ops/flashprefill_varlen_func.py:106-409,615-698
+ *   fp_select              the normalise + threshold + compaction half of fp_search, fed with
+ *                          caller-supplied fp32 block scores (p, m)
+ *                          ops/flashprefill_native_forward.py:347-403, ops/flashprefill_varlen_func.py:240-409,656
+ *   fp_sparse_attn_fwd     _flash_forward / _flash_block_sparse_varlen
+ *                          ops/flashprefill_native_forward.py:227-344, ops/flashprefill_varlen_func.py:449-575
+ */
+#ifndef FLASHPREFILL_H
+#define FLASHPREFILL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FP_OK 0
+#define FP_E_INVALID_ARG (-1)   /* shapes, strides, alignment or scalars out of range */
+#define FP_E_UNSUPPORTED (-2)   /* valid for the reference but not built here (e.g. fp32) */
+#define FP_E_LAUNCH (-3)        /* a HIP launch or runtime call failed */
+
+#define FP_DTYPE_BF16 0
+#define FP_DTYPE_F16 1
+
+/* Device-side status flags (`fp_status` word in the workspace, see
+ * fp_read_status): set by the kernels when cu_seqlens disagrees with the host
+ * sizes; the affected sequences are skipped and their output left untouched. */
+#define FP_STATUS_SEQ_TOO_LONG 1u   /* a sequence is longer than max_seq_len */
+#define FP_STATUS_BAD_CU_SEQLENS 2u /* cu_seqlens decreasing or beyond total_tokens */
+
+typedef struct fp_problem {
+    /* Q (T, Hq, d), K/V (T, Hkv, d), O (T, Hq, d): device pointers, head dim
+     * contiguous, strides in elements. The batched entry point (B, S, H, d)
+     * is the same memory with token stride H*d and uniform sequence length. */
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    int64_t q_stride_tok, q_stride_head;
+    int64_t k_stride_tok, k_stride_head;
+    int64_t v_stride_tok, v_stride_head;
+    int64_t o_stride_tok, o_stride_head;
+    /* Sequences: cu_seqlens (device, int32, batch+1 entries) or, when NULL,
+     * `batch` sequences of `uniform_seq_len` tokens each. */
+    const int32_t* cu_seqlens;
+    int32_t batch;
+    int32_t uniform_seq_len;
+    int32_t max_seq_len;   /* host upper bound of every sequence length */
+    int64_t total_tokens;  /* T = number of rows of q/k/v/o */
+    int32_t num_q_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim;      /* 64 or 128 */
+    int32_t dtype;         /* FP_DTYPE_BF16 or FP_DTYPE_F16 */
+    int32_t block_size;    /* 128 */
+    /* selection */
+    float alpha;
+    int32_t attention_sink;
+    int32_t window_size;
+    int32_t last_n_block;
+    int32_t native_normalize; /* 1: S /= (sum S + 1e-9) (flash_prefill); 0: varlen */
+    int32_t min_budget;       /* native top-k floor; 0 everywhere in the reference */
+} fp_problem;
+
+/* Where each intermediate lives inside the workspace (byte offsets), with the
+ * index arithmetic the kernels use:
+ *   pooled K   mk[(tile(b) + j) * Hkv * d + kvh * d + x]            (dtype)
+ *   counts     cnt[h * nb_sum_cap + tile(b) + i]                    (int32)
+ *   lists      idx[h * tri_cap + tri(b) + i*(i+1)/2 + n], n < cnt   (int32, ascending j)
+ *   p/m dumps  same triangular index with j in place of n           (fp32)
+ * tile(b) = sum_{b'<b} NB_b', tri(b) = sum_{b'<b} NB_b'(NB_b'+1)/2, read back
+ * from seq_tile / seq_tri (int64, batch+1 entries). Entries of skipped or
+ * never-selected slots are not written (the workspace is not cleared). */
+typedef struct fp_ws_layout {
+    size_t total_bytes;
+    size_t status_off;   /* uint32 status flags */
+    size_t seq_tile_off; /* int64[batch+1] */
+    size_t seq_tri_off;  /* int64[batch+1] */
+    size_t seq_start_off; /* int64[batch]: first token of each sequence */
+    size_t seq_len_off;  /* int32[batch]: tokens (0 for a skipped sequence) */
+    size_t items_off;    /* int32[2 * nb_sum_cap]: (b, i) heaviest first */
+    size_t mk_off;
+    size_t cnt_off;
+    size_t idx_off;
+    int64_t nb_sum_cap;  /* >= sum_b NB_b */
+    int64_t tri_cap;     /* >= sum_b NB_b (NB_b + 1) / 2 */
+    int32_t nb_max;      /* ceil(max_seq_len / block_size) */
+} fp_ws_layout;
+
+/* Validate `p` and compute the workspace layout (no device work). */
+int fp_workspace_layout(const fp_problem* p, fp_ws_layout* out);
+size_t fp_workspace_bytes(const fp_problem* p);
+
+/* Whole operator: plan -> pool K -> search (score + select) -> attention.
+ * Writes O in place. Replaces flash_prefill_varlen_func / flash_prefill. */
+int fp_flashprefill(const fp_problem* p, void* workspace, void* stream);
+
+/* Stages, in the order fp_flashprefill runs them. Each reads what the previous
+ * ones wrote into the same workspace. */
+int fp_plan(const fp_problem* p, void* workspace, void* stream);
+int fp_pool_k(const fp_problem* p, void* workspace, void* stream);
+/* dump_p / dump_m: optional fp32 arrays of Hq * tri_cap entries that receive
+ * the block scores in the triangular layout above (NULL to skip). */
+int fp_search(const fp_problem* p, void* workspace, float* dump_p, float* dump_m, void* stream);
+/* Selection only, from caller-supplied fp32 block scores in the triangular
+ * layout (requires fp_plan to have run on this workspace). */
+int fp_select(const fp_problem* p, void* workspace, const float* p_scores,
+              const float* m_scores, void* stream);
+int fp_sparse_attn_fwd(const fp_problem* p, void* workspace, void* stream);
+
+/* Copy the device status word to the host (synchronises `stream`). */
+int fp_read_status(const fp_problem* p, void* workspace, void* stream, uint32_t* status);
+
+const char* fp_last_error(void);
+/* ABI version: bump on any change to fp_problem or fp_ws_layout. */
+int fp_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FLASHPREFILL_H */

@@ -1,0 +1,103 @@
+"""CPU checks of the C ABI: the library loads, exports every entry point that
+include/flashprefill.h declares, and validates arguments on the host (no GPU
+call is made: the descriptors below are rejected before any launch, and the
+layout query is pure host arithmetic)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from flashprefill_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "flashprefill.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fp_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_entry_points():
+    assert set(_declared()) == set(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.fp_abi_version() == _lib.ABI_VERSION
+
+
+def _problem(**kw):
+    P = _lib.FpProblem()
+    P.q = P.k = P.v = P.o = 0x10000
+    P.q_stride_tok, P.q_stride_head = 8 * 128, 128
+    P.k_stride_tok, P.k_stride_head = 2 * 128, 128
+    P.v_stride_tok, P.v_stride_head = 2 * 128, 128
+    P.o_stride_tok, P.o_stride_head = 8 * 128, 128
+    P.cu_seqlens = 0x20000
+    P.batch, P.max_seq_len, P.total_tokens = 3, 4096, 6000
+    P.num_q_heads, P.num_kv_heads, P.head_dim = 8, 2, 128
+    P.dtype, P.block_size, P.alpha = _lib.FP_DTYPE_BF16, 128, 0.18
+    P.attention_sink, P.window_size, P.last_n_block = 2, 4, 2
+    for k, v in kw.items():
+        setattr(P, k, v)
+    return P
+
+
+def _layout(P):
+    L = _lib.FpWsLayout()
+    rc = _lib.load().fp_workspace_layout(ctypes.byref(P), ctypes.byref(L))
+    return rc, L
+
+
+def test_layout_bounds():
+    rc, L = _layout(_problem())
+    assert rc == _lib.FP_OK
+    assert L.nb_max == 32
+    assert L.nb_sum_cap == (6000 + 127 * 3) // 128
+    # worst packing: full sequences of 32 blocks + remainder
+    cap = L.nb_sum_cap
+    assert L.tri_cap == (cap // 32) * 32 * 33 // 2 + (cap % 32) * (cap % 32 + 1) // 2
+    offs = [L.status_off, L.seq_tile_off, L.seq_tri_off, L.seq_start_off, L.seq_len_off,
+            L.items_off, L.mk_off, L.cnt_off, L.idx_off]
+    assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
+    assert L.total_bytes >= L.idx_off + 4 * 8 * L.tri_cap
+    assert _lib.load().fp_workspace_bytes(ctypes.byref(_problem())) == L.total_bytes
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("dtype", 7, _lib.FP_E_UNSUPPORTED),
+    ("head_dim", 96, _lib.FP_E_UNSUPPORTED),
+    ("block_size", 64, _lib.FP_E_UNSUPPORTED),
+    ("num_kv_heads", 3, _lib.FP_E_INVALID_ARG),
+    ("batch", 0, _lib.FP_E_INVALID_ARG),
+    ("max_seq_len", 0, _lib.FP_E_INVALID_ARG),
+    ("q", 0x10002, _lib.FP_E_INVALID_ARG),
+    ("k_stride_tok", 100, _lib.FP_E_INVALID_ARG),
+    ("min_budget", 4, _lib.FP_E_UNSUPPORTED),
+    ("native_normalize", 2, _lib.FP_E_INVALID_ARG),
+])
+def test_invalid_arguments_rejected_on_host(field, value, code):
+    rc, _ = _layout(_problem(**{field: value}))
+    assert rc == code
+    assert _lib.load().fp_last_error()
+
+
+def test_uniform_batch_bounds():
+    rc, _ = _layout(_problem(cu_seqlens=None, uniform_seq_len=2000, batch=3))
+    assert rc == _lib.FP_OK
+    rc, _ = _layout(_problem(cu_seqlens=None, uniform_seq_len=5000, batch=1))
+    assert rc == _lib.FP_E_INVALID_ARG  # longer than max_seq_len
+
+
+def test_check_maps_codes_to_python_exceptions():
+    rc, _ = _layout(_problem(head_dim=96))
+    with pytest.raises(NotImplementedError):
+        _lib.check(rc)
+    rc, _ = _layout(_problem(num_kv_heads=3))
+    with pytest.raises(ValueError):
+        _lib.check(rc)

@@ -1,0 +1,115 @@
+"""GPU tests of the public operator surface (the reference's two entry points)
+and of the C ABI's error / status behaviour."""
+
+import pytest
+import torch
+
+from flashprefill_amd import FlashPrefillCall, flash_prefill, flash_prefill_varlen_func
+from flashprefill_amd import _lib
+from oracle import flashprefill_oracle as O
+from tests._parity import OUT_MAX_ABS, OUT_MEAN_ABS
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _rand(shape, seed, dtype=torch.bfloat16, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+def _close(out, ref, flips_ok=True):
+    d = (out.float().cpu() - ref.float()).abs()
+    assert not torch.isnan(d).any()
+    assert d.mean().item() <= OUT_MEAN_ABS, d.mean().item()
+    assert d.max().item() <= OUT_MAX_ABS, d.max().item()
+
+
+def test_varlen_api_matches_oracle_and_is_deterministic():
+    lens = [513, 1024, 77]
+    T = sum(lens)
+    q, k, v = _rand((T, 8, 128), 1, scale=1.5), _rand((T, 2, 128), 2, scale=1.5), _rand((T, 2, 128), 3)
+    cu = torch.tensor([0, 513, 1537, T], dtype=torch.int32)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    o1 = torch.empty_like(qd)
+    o2 = torch.empty_like(qd)
+    flash_prefill_varlen_func(qd, kd, vd, o1, cu.to(DEV), 1024, 0.18)
+    flash_prefill_varlen_func(qd, kd, vd, o2, cu.to(DEV), 1024, 0.18, 128, 2, 4, 2)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    ref = O.flash_prefill_varlen_func(q, k, v, cu, 1024, 0.18).out
+    _close(o1, ref)
+
+
+def test_native_batched_api_matches_oracle():
+    B, S, Hq, Hkv, d = 2, 1000, 8, 8, 128
+    q, k, v = _rand((B, S, Hq, d), 4, scale=1.5), _rand((B, S, Hkv, d), 5, scale=1.5), _rand((B, S, Hkv, d), 6)
+    out = torch.empty(B, S, Hq, d, dtype=torch.bfloat16, device=DEV)
+    flash_prefill(q.to(DEV), k.to(DEV), v.to(DEV), out, 128, 2, 4, 0.7, 2, 0)
+    torch.cuda.synchronize()
+    ref = O.flash_prefill(q, k, v, 128, 2, 4, 0.7, 2, 0).out
+    _close(out, ref)
+
+
+def test_strided_inputs_match_contiguous():
+    # q/k/v carved out of one fused qkv projection output, as vLLM does
+    T, Hq, Hkv, d = 900, 8, 2, 128
+    qkv = _rand((T, Hq + 2 * Hkv, d), 7, scale=1.5).to(DEV)
+    q, k, v = qkv[:, :Hq], qkv[:, Hq:Hq + Hkv], qkv[:, Hq + Hkv:]
+    assert not q.is_contiguous()
+    cu = torch.tensor([0, 400, T], dtype=torch.int32, device=DEV)
+    o_strided = torch.empty(T, 2 * Hq, d, dtype=torch.bfloat16, device=DEV)[:, :Hq]
+    o_ref = torch.empty(T, Hq, d, dtype=torch.bfloat16, device=DEV)
+    flash_prefill_varlen_func(q, k, v, o_strided, cu, 500, 0.18)
+    flash_prefill_varlen_func(q.contiguous(), k.contiguous(), v.contiguous(), o_ref, cu, 500, 0.18)
+    torch.cuda.synchronize()
+    assert torch.equal(o_strided, o_ref)
+
+
+def test_all_blocks_selected_is_dense_causal():
+    T, Hq, Hkv, d = 640, 4, 2, 64
+    q, k, v = _rand((T, Hq, d), 8, scale=1.5), _rand((T, Hkv, d), 9, scale=1.5), _rand((T, Hkv, d), 10)
+    o = torch.empty(T, Hq, d, dtype=torch.bfloat16, device=DEV)
+    cu = torch.tensor([0, T], dtype=torch.int32, device=DEV)
+    flash_prefill_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), o, cu, T, 0.0)  # alpha 0: S >= 0
+    torch.cuda.synchronize()
+    qq = q.double().permute(1, 0, 2)
+    kk = k.double().permute(1, 0, 2).repeat_interleave(2, 0)
+    vv = v.double().permute(1, 0, 2).repeat_interleave(2, 0)
+    ref = torch.nn.functional.scaled_dot_product_attention(qq, kk, vv, is_causal=True)
+    _close(o, ref.permute(1, 0, 2))
+
+
+def test_status_flags_and_untouched_output():
+    T, Hq, Hkv, d = 1000, 4, 1, 128
+    q, k, v = _rand((T, Hq, d), 11).to(DEV), _rand((T, Hkv, d), 12).to(DEV), _rand((T, Hkv, d), 13).to(DEV)
+    o = torch.full((T, Hq, d), 7.0, dtype=torch.bfloat16, device=DEV)
+    cu = torch.tensor([0, 300, 1000], dtype=torch.int32, device=DEV)  # second seq has 700 > 512
+    call = FlashPrefillCall(q, k, v, o, cu, 512, alpha=0.18)
+    call.run()
+    assert call.status() == _lib.FP_STATUS_SEQ_TOO_LONG
+    assert (o[300:] == 7.0).all()
+    assert not (o[:300] == 7.0).all()
+    cu_bad = torch.tensor([0, 300, 2000], dtype=torch.int32, device=DEV)
+    call = FlashPrefillCall(q, k, v, o, cu_bad, 2000, alpha=0.18)
+    call.run()
+    assert call.status() & _lib.FP_STATUS_BAD_CU_SEQLENS
+
+
+def test_error_paths():
+    T = 256
+    q = torch.zeros(T, 4, 128, dtype=torch.float32, device=DEV)
+    cu = torch.tensor([0, T], dtype=torch.int32, device=DEV)
+    with pytest.raises(NotImplementedError):
+        flash_prefill_varlen_func(q, q[:, :1], q[:, :1], q.clone(), cu, T, 0.1)
+    qb = q.to(torch.bfloat16)
+    with pytest.raises(ValueError):
+        flash_prefill_varlen_func(qb, qb[:, :3].contiguous(), qb[:, :3].contiguous(), qb.clone(),
+                                  cu, T, 0.1)
+    q96 = torch.zeros(T, 4, 96, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(NotImplementedError):
+        flash_prefill_varlen_func(q96, q96[:, :1].contiguous(), q96[:, :1].contiguous(),
+                                  q96.clone(), cu, T, 0.1)
+    with pytest.raises(NotImplementedError):
+        flash_prefill_varlen_func(qb, qb[:, :1].contiguous(), qb[:, :1].contiguous(), qb.clone(),
+                                  cu, T, 0.1, block_size=64)
