@@ -1,0 +1,223 @@
+"""Benchmark of the FlashPrefill gfx950 path on BASELINE config 3.
+
+One step = one full ``flash_prefill_varlen_func`` call (plan -> pool K ->
+search -> block-sparse attention) over a 131072-token single sequence with
+Llama-3-8B head shapes (32 q / 8 kv heads, d = 128, bf16, causal, block 128),
+inputs resident in HBM. Prints ONE JSON line (rank 0). See DESIGN.md for the
+definitions of every figure.
+
+    python bench.py [--gpus 1] [--steps 10] [--warmup 3]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = ("128K prefill attn latency (ms) + effective TFLOPS, speedup vs dense at 1 MI355X")
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBPS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--seq-len", type=int, default=131072)
+    ap.add_argument("--seed", type=int, default=128)
+    ap.add_argument("--alpha", type=float, default=0.18)
+    ap.add_argument("--no-dense", action="store_true", help="skip the dense baselines")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0,
+                    help="time budget of the CPU baseline sample")
+    return ap.parse_args()
+
+
+def timed(fn, reps, stream=None):
+    """Average milliseconds of fn() over reps, with HIP events on the current stream."""
+    import torch
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def dense_causal_flops(S, Hq, d):
+    return 2.0 * d * Hq * S * (S + 1)
+
+
+def cpu_baseline(q, k, v, alpha, budget_s):
+    """The oracle (a CPU restatement of the reference algorithm) on a bounded
+    sample of the same workload: every query head, q-blocks visited from the
+    last one down in strides of 64, until ``budget_s`` seconds are used.
+    Rate = dense-causal FLOPs of the sampled rows / CPU time (same unit as
+    ``value``)."""
+    import torch
+    from oracle import flashprefill_oracle as O
+    torch.set_num_threads(os.cpu_count() or 1)
+    S, Hq, d = q.shape
+    nb = (S + 127) // 128
+    qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
+    t0 = time.perf_counter()
+    mk = O.pool_k(kc)
+    rows_done, flops = 0, 0.0
+    stride_rows = [i for i in range(nb - 1, -1, -64)]
+    for i in stride_rows:
+        rows = [(h, i) for h in range(Hq)]
+        O.flashprefill_rows(qc, kc, vc, rows, alpha=alpha, attention_sink=2, window=4,
+                            last_n=2, native=False, mk=mk)
+        rows_done += len(rows)
+        q0, q1 = i * 128, min(S, (i + 1) * 128)
+        flops += Hq * 4.0 * d * sum(range(q0 + 1, q1 + 1))
+        if time.perf_counter() - t0 > budget_s:
+            break
+    el = time.perf_counter() - t0
+    return {
+        "value": flops / el / 1e12,
+        "unit": "TFLOP/s (effective)",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"oracle (pool K of all {nb} blocks, then score+select+attention) on "
+                   f"{rows_done} (head, q-block) rows of the same 128K input: all {Hq} heads x "
+                   f"q-blocks {nb - 1}, {nb - 65}, ... ; {el:.1f} s on "
+                   f"{platform.processor() or platform.machine()}, os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (one MI355X per box); "
+              "--gpus N with N > 1 is not supported", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from flashprefill_amd import synth
+    from flashprefill_amd.runtime import FlashPrefillCall
+
+    dev = torch.device("cuda:0")
+    S = args.seq_len
+    spec = synth.llama_spec(S, seed=args.seed)
+    print(f"bench: generating {S}-token structured input on {dev}", file=sys.stderr, flush=True)
+    q, k, v, cu = synth.make_inputs(spec, device=dev)
+    Hq, Hkv, d = spec.num_q_heads, spec.num_kv_heads, spec.head_dim
+    o = torch.empty_like(q)
+    call = FlashPrefillCall(q, k, v, o, cu, S, alpha=args.alpha, attention_sink=2,
+                            window_size=4, last_n_block=2)
+
+    for _ in range(args.warmup):
+        call.run()
+    torch.cuda.synchronize()
+    print("bench: timing", file=sys.stderr, flush=True)
+    ms_total = timed(call.run, args.steps)
+
+    def search_stage():
+        call.plan()
+        call.pool()
+        call.search()
+
+    ms_search = timed(search_stage, max(3, args.steps))
+    ms_attn = timed(call.attn, max(3, args.steps))
+    assert call.status() == 0
+
+    nb = (S + 127) // 128
+    tile, _, _, _ = call.seq_tables()
+    n_exec = int(call.counts()[:, :tile[-1]].sum().item())
+    causal_blocks = Hq * nb * (nb + 1) // 2
+    density = n_exec / causal_blocks
+    exec_flops = 4.0 * 128 * 128 * d * n_exec
+    dense_flops = dense_causal_flops(S, Hq, d)
+    exec_tflops = exec_flops / (ms_attn * 1e-3) / 1e12
+    eff_tflops = dense_flops / (ms_total * 1e-3) / 1e12
+    search_bytes = (q.numel() + k.numel()) * q.element_size()
+    search_gbps = search_bytes / (ms_search * 1e-3) / 1e9
+
+    dense = {}
+    if not args.no_dense:
+        print("bench: dense baselines", file=sys.stderr, flush=True)
+        # our own kernel with every causal block selected (alpha = 0 keeps S >= 0)
+        o2 = torch.empty_like(q)
+        dcall = FlashPrefillCall(q, k, v, o2, cu, S, alpha=0.0, attention_sink=2,
+                                 window_size=4, last_n_block=2)
+        dcall.plan(); dcall.pool(); dcall.search()
+        dcall.attn()
+        dense["own_all_blocks_attn_ms"] = timed(dcall.attn, 1)
+        dense["own_all_blocks_tflops"] = dense_flops / (dense["own_all_blocks_attn_ms"] * 1e-3) / 1e12
+        del o2, dcall
+        try:
+            from torch.nn.attention import SDPBackend, sdpa_kernel
+            qh = q.transpose(0, 1).unsqueeze(0)
+            kh = k.repeat_interleave(Hq // Hkv, dim=1).transpose(0, 1).unsqueeze(0)
+            vh = v.repeat_interleave(Hq // Hkv, dim=1).transpose(0, 1).unsqueeze(0)
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+                torch.nn.functional.scaled_dot_product_attention(qh, kh, vh, is_causal=True)
+                dense["sdpa_flash_ms"] = timed(
+                    lambda: torch.nn.functional.scaled_dot_product_attention(
+                        qh, kh, vh, is_causal=True), 2)
+            dense["sdpa_flash_tflops"] = dense_flops / (dense["sdpa_flash_ms"] * 1e-3) / 1e12
+            del qh, kh, vh
+        except Exception as exc:  # the flash backend is the only one that fits 128K
+            dense["sdpa_flash_error"] = f"{type(exc).__name__}: {exc}"[:200]
+        cands = [x for x in (dense.get("sdpa_flash_ms"), dense.get("own_all_blocks_attn_ms"))
+                 if x]
+        if cands:
+            dense["fastest_dense_ms"] = min(cands)
+            dense["speedup_vs_dense"] = min(cands) / ms_total
+
+    cpu = None
+    if not args.no_cpu:
+        print("bench: CPU baseline (oracle sample)", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(q, k, v, args.alpha, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": round(eff_tflops, 3),
+        "unit": "TFLOP/s (effective: dense-causal FLOPs / time per prefill)",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_total, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": ("synthetic: seeded structured Q/K/V ~ N(0,1)/sqrt(d) with sinks, 64 stripe "
+                 "runs, rotary local band, topic segments, 8 hot blocks/head "
+                 "(flashprefill_amd/synth.py)"),
+        "config": {"workload": "BASELINE config 3: 131072-token single-sequence prefill attention, "
+                               "Llama-3-8B heads", "seq_len": S, "num_q_heads": Hq,
+                   "num_kv_heads": Hkv, "head_dim": d, "block_size": 128, "alpha": args.alpha,
+                   "attention_sink": 2, "window_size": 4, "last_n_block": 2, "seed": args.seed},
+        "t_search_ms": round(ms_search, 4),
+        "t_attn_ms": round(ms_attn, 4),
+        "search_share": round(ms_search / ms_total, 4),
+        "density": round(density, 5),
+        "executed_blocks": n_exec,
+        "executed_tflops": round(exec_tflops, 2),
+        "search_algorithmic_GBps": round(search_gbps, 1),
+        "dense": {k2: (round(v2, 4) if isinstance(v2, float) else v2) for k2, v2 in dense.items()},
+        "roofline": {"bound": "mfma", "kernel": "k_attn (block-sparse attention)",
+                     "achieved": round(exec_tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(exec_tflops / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

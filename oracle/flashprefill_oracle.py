@@ -314,6 +314,82 @@ def dense_masked_attention_fp64(q_seq: torch.Tensor, k_seq: torch.Tensor,
     return out
 
 
+def flashprefill_rows(q_seq: torch.Tensor, k_seq: torch.Tensor, v_seq: torch.Tensor,
+                      rows: Sequence[Tuple[int, int]], *, alpha: float, attention_sink: int,
+                      window: int, last_n: int, native: bool, block: int = 128,
+                      mk: Optional[torch.Tensor] = None
+                      ) -> Dict[Tuple[int, int], Tuple[torch.Tensor, torch.Tensor]]:
+    """The whole pipeline restricted to some (head, q-block) rows of one
+    sequence: pooled K (all blocks), the block scores of each listed row,
+    its normalisation and selection, and its attention output. Same arithmetic
+    as block_score / normalize_scores / select_blocks / sparse_attention
+    applied to one row; used to time a bounded sample of a long sequence.
+    Returns {(h, i): (sel_row (NB,) bool, out (rows_in_block, d))}."""
+    S, Hq, d = q_seq.shape
+    Hkv = k_seq.shape[1]
+    G = Hq // Hkv
+    nb = num_blocks(S, block)
+    c = sm_scale_f32(d)
+    if mk is None:
+        mk = pool_k(k_seq, block)
+    ninf = torch.tensor(float("-inf"))
+    r = torch.arange(block).view(block, 1)
+    pos = torch.arange(block)
+    diag_mask = pos.view(block, 1) >= pos.view(1, block)
+    res = {}
+    for h, i in rows:
+        kvh = h // G
+        q0, q1 = i * block, min(S, (i + 1) * block)
+        qi = torch.zeros(block, d, dtype=torch.float64)
+        qi[:q1 - q0] = q_seq[q0:q1, h].double()
+        raw = (qi @ mk[:i + 1, kvh].double().T).float()  # (block, i+1)
+        s = raw * c
+        mask = (block * i + r) >= (block * torch.arange(i + 1).view(1, -1) + block - 1)
+        s = torch.where(mask, s, ninf)
+        m_row = s.max(dim=0).values
+        e = torch.where(mask, torch.exp2((s - m_row.view(1, -1)).double()),
+                        torch.zeros((), dtype=torch.float64))
+        p_row = e.sum(dim=0).float()
+        # normalisation and selection of row i (all j <= i are causal)
+        M = m_row.max()
+        S_row = p_row * exp2_f32(m_row - M)
+        if native:
+            tot = S_row.double().sum().float()
+            S_row = S_row / (tot + _f32(1e-9))
+        thr = S_row.max() * _f32(alpha)
+        jj = torch.arange(i + 1)
+        keep = (S_row >= thr) | (jj < attention_sink) | ((i - jj) < window) | (i >= nb - last_n)
+        sel_row = torch.zeros(nb, dtype=torch.bool)
+        sel_row[:i + 1] = keep
+        # attention of this row over its selected blocks
+        js = torch.nonzero(sel_row).flatten().tolist()
+        m_i = torch.full((block,), float("-inf"))
+        l_i = torch.ones(block)
+        acc = torch.zeros(block, d)
+        for j in js:
+            k0, k1 = j * block, min(S, (j + 1) * block)
+            kj = torch.zeros(block, d, dtype=torch.float64)
+            vj = torch.zeros(block, d, dtype=torch.float32)
+            kj[:k1 - k0] = k_seq[k0:k1, kvh].double()
+            vj[:k1 - k0] = v_seq[k0:k1, kvh].float()
+            qk = (qi @ kj.T).float()
+            if j == i:
+                qk = torch.where(diag_mask, qk, ninf)
+            qk = qk * c
+            m_new = torch.maximum(m_i, qk.max(dim=1).values)
+            p = exp2_f32(qk - m_new.view(block, 1))
+            lij = p.double().sum(dim=1).float()
+            a_ = exp2_f32(m_i - m_new)
+            a_ = torch.where(torch.isnan(a_), torch.ones(()), a_)
+            acc = acc * a_.view(block, 1)
+            l_i = l_i * a_ + lij
+            acc = acc + (p.to(v_seq.dtype).float().double() @ vj.double()).float()
+            m_i = m_new
+        out = (acc * (1.0 / l_i).view(block, 1))[:q1 - q0].to(q_seq.dtype)
+        res[(h, i)] = (sel_row, out)
+    return res
+
+
 # ---------------------------------------------------------------------------
 # layouts of the selection (…native_forward.py:377-385; …varlen_func.py:683-698)
 # ---------------------------------------------------------------------------

@@ -306,3 +306,21 @@ def test_index_layouts():
             js = torch.nonzero(sel[0, h, i]).flatten().to(torch.int32)
             assert torch.equal(flat[pos:pos + js.numel()], js)
             pos += js.numel()
+
+
+@pytest.mark.parametrize("native", [False, True])
+def test_rows_pipeline_equals_full_pipeline(native):
+    # the bounded-sample helper used for CPU timing computes exactly the full rows
+    g = torch.Generator().manual_seed(71)
+    S, Hq, Hkv, d = 700, 4, 2, 32
+    q = (torch.randn(S, Hq, d, generator=g) * 2).to(torch.bfloat16)
+    k = (torch.randn(S, Hkv, d, generator=g) * 2).to(torch.bfloat16)
+    v = torch.randn(S, Hkv, d, generator=g).to(torch.bfloat16)
+    out, tr = O.flashprefill_sequence(q, k, v, alpha=0.3, attention_sink=1, window=2, last_n=1,
+                                      native=native)
+    rows = [(h, i) for h in range(Hq) for i in range(6)]
+    res = O.flashprefill_rows(q, k, v, rows, alpha=0.3, attention_sink=1, window=2, last_n=1,
+                              native=native)
+    for (h, i), (sel_row, o_row) in res.items():
+        assert torch.equal(sel_row, tr.sel[h, i])
+        assert torch.equal(o_row, out[i * 128:(i + 1) * 128, h])
