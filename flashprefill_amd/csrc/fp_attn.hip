@@ -17,25 +17,221 @@
 //                                        (the MFMA k order is permuted
 //                                        identically on both operands)
 //
-// all on v_mfma_f32_32x32x16 (bf16 or fp16 in, fp32 accumulate). K and V
-// blocks (128 keys x d) are gathered by index into LDS with a row-dependent
-// 16-byte-chunk XOR swizzle that keeps both the K operand reads and the
-// transposing V reads free of bank conflicts.
+// all on v_mfma_f32_32x32x16 (bf16 or fp16 in, fp32 accumulate).
+//
+// K and V blocks (128 keys x d) are gathered by index with direct-to-LDS
+// loads (global_load_lds_dwordx4, no VGPR staging) into one K and one V
+// buffer per workgroup (2 x 32 KB at d = 128, two workgroups per CU). The two
+// buffers are pipelined against each other: the next block's K streams in
+// while this block's softmax and P.V run, the next block's V while the next
+// S = K.Q^T runs. Rows are stored with a 16-byte-chunk XOR swizzle chosen for
+// the 64-bank LDS so that the K operand reads (16 rows, one chunk column per
+// cycle) and the transposing V reads (4 rows x 4 chunks) are conflict free.
 //
 // Numerics follow the reference loop: m starts at -inf and l at 1.0, one
 // 128-key tile per selected block, alpha = exp2(m_old - m_new) with NaN -> 1,
 // l accumulates the fp32 p, P is rounded to the input dtype before P.V, the
-// diagonal block masks key > query, and O = acc * (1/l).
+// diagonal block masks key > query, and O = acc * (1/l). The accumulator is
+// rescaled only when some row's max moved (alpha == 1 makes it a no-op).
 #include "fp_internal.h"
 
 namespace fp {
 
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void gbl_void_t;
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
-// element offset of (row r, column x) in a 128 x D tile
+// chunk swizzle of row r in a 128 x D tile (D/8 chunks of 16 bytes per row)
+template <int D>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+  else return (r >> 1) & 7;
+}
+
 template <int D>
 __device__ __forceinline__ int tile_elem(int r, int x) {
-  return r * D + ((((x >> 3) ^ swz(r))) << 3) + (x & 7);
+  return r * D + ((((x >> 3) ^ swz<D>(r))) << 3) + (x & 7);
+}
+
+// two fp32 -> packed pair of the input type (round to nearest even)
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float a, float b);
+template <>
+__device__ __forceinline__ uint32_t pack2<BF16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<F16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+}
+
+// wait for this wave's vector-memory ops down to N outstanding, then barrier
+template <int N>
+__device__ __forceinline__ void vm_barrier() {
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
+  else asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+}
+// all of this wave's LDS reads are done, then barrier (buffer may be refilled)
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Direct-to-LDS loads of one 128 x D tile (block j of a K or V head). Wave w
+// fills the 1 KB LDS slices w*NI .. w*NI+NI-1; in each slice lane l writes
+// physical chunk l % CH of row slice*RPW + l / CH, so it fetches logical
+// chunk (l % CH) ^ swz(row) of that row. Because swz(row) only depends on
+// (l / CH) and on q modulo a small period, the per-lane part of the source
+// address is a 32-bit byte offset from a small precomputed table and the rest
+// is a wave-uniform (scalar) base.
+template <int D>
+struct TileLanes {
+  static constexpr int CH = D / 8;      // chunks per row
+  static constexpr int RPW = 64 / CH;   // rows per wave instruction
+  static constexpr int NI = CH / 2;     // instructions per wave per tile
+  static constexpr int PER = D == 128 ? 4 : 2;  // period of swz over q
+  uint32_t off[PER];                    // per-lane byte offsets
+  __device__ __forceinline__ void init(int64_t stride, int w, int lane) {
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int r = (w * NI + q) * RPW + lane / CH;
+      const int c = (lane % CH) ^ swz<D>(r);
+      off[q] = static_cast<uint32_t>(((lane / CH) * stride + 8 * c) * 2);
+    }
+  }
+};
+
+template <int D>
+__device__ __forceinline__ void issue_tile(uint4* lds, const uint16_t* base, int64_t stride,
+                                           const TileLanes<D>& tl, int j, int L, int w,
+                                           int lane) {
+  constexpr int CH = TileLanes<D>::CH, RPW = TileLanes<D>::RPW, NI = TileLanes<D>::NI;
+  if ((j + 1) * kBlock <= L) {
+#pragma unroll
+    for (int q = 0; q < NI; ++q) {
+      const int slot = w * NI + q;
+      const char* sbase = reinterpret_cast<const char*>(base) +
+                          static_cast<int64_t>(j * kBlock + slot * RPW) * stride * 2;
+      const char* src = sbase + tl.off[q % TileLanes<D>::PER];
+      __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)(lds + slot * 64), 16, 0, 0);
+    }
+  } else {  // partial last block: rows past the end read row L-1 (masked keys, p = 0)
+#pragma unroll
+    for (int q = 0; q < NI; ++q) {
+      const int slot = w * NI + q;
+      const int r = slot * RPW + lane / CH;
+      const int c = (lane % CH) ^ swz<D>(r);
+      const int gk = min(j * kBlock + r, L - 1);
+      const uint16_t* src = base + static_cast<int64_t>(gk) * stride + 8 * c;
+      __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)(lds + slot * 64), 16, 0, 0);
+    }
+  }
+}
+
+template <typename T, int D>
+struct AttnState {
+  f32x16 o[D / 32];
+  float m_run;
+  float l_part;
+};
+
+// One selected block: S = K.Q^T, online softmax, O += V^T.P^T, and the
+// pipelined refills of the K / V buffers with block `jn` (when jn >= 0).
+template <typename T, int D, bool DIAG>
+__device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T::vec8* qb,
+                                           const uint4* sk, uint4* sk_w, const uint16_t* sv16,
+                                           uint4* sv_w, const uint16_t* kbase,
+                                           const uint16_t* vbase, int64_t kst, int64_t vst,
+                                           const TileLanes<D>& tk, const TileLanes<D>& tv,
+                                           int jn, int L, float c, int w, int lane) {
+  constexpr int CH = D / 8;
+  constexpr int KS = D / 16;
+  constexpr int DT = D / 32;
+  const int half = lane >> 5, l32 = lane & 31;
+  const int qrow = 32 * w + l32;
+
+  vm_barrier<CH / 2>();  // K of this block has landed (V may still be in flight)
+  f32x16 s[4];
+#pragma unroll
+  for (int t4 = 0; t4 < 4; ++t4) {
+    s[t4] = f32x16{};
+    const int r = 32 * t4 + l32;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const uint4 kop = sk[r * CH + ((2 * ks + half) ^ swz<D>(r))];
+      s[t4] = T::mfma32(as_vec8<T>(kop), qb[ks], s[t4]);
+    }
+  }
+  lds_barrier();  // every wave is done with the K buffer
+  if (jn >= 0) issue_tile<D>(sk_w, kbase, kst, tk, jn, L, w, lane);
+
+  if constexpr (DIAG) {  // key > query is masked on the diagonal block
+#pragma unroll
+    for (int t4 = 0; t4 < 4; ++t4)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int key = 32 * t4 + 8 * (v >> 2) + 4 * half + (v & 3);
+        if (key > qrow) s[t4][v] = -INFINITY;
+      }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int t4 = 0; t4 < 4; ++t4)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[t4][v]);
+  mx = fmaxf(mx, xor32_f(mx));
+  const float m_new = fmaxf(st.m_run, mx * c);
+  float alpha = __builtin_amdgcn_exp2f(st.m_run - m_new);
+  if (alpha != alpha) alpha = 1.0f;
+  float psum = 0.0f;
+#pragma unroll
+  for (int t4 = 0; t4 < 4; ++t4)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const float p = __builtin_amdgcn_exp2f(fmaf(s[t4][v], c, -m_new));
+      s[t4][v] = p;
+      psum += p;
+    }
+  st.l_part = st.l_part * alpha + psum;
+  st.m_run = m_new;
+  if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) st.o[dt][v] *= alpha;
+  }
+
+  if (jn >= 0) vm_barrier<CH / 2>(); else vm_barrier<0>();  // V of this block has landed
+  // O^T += V^T . P^T over 8 steps of 16 keys. B element e of lane (q, half)
+  // is key 16 u + (e < 4 ? 4 half + e : 8 + 4 half + e - 4); the A operand
+  // (V^T) is read in the same key order with two transposing reads.
+  const int g16 = lane >> 4, i16 = lane & 15;
+  const int tr_row = 4 * (g16 >> 1) + (i16 >> 2);
+  const int tr_col = 16 * (g16 & 1) + 4 * (i16 & 3);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int t4 = u >> 1, hh = u & 1;
+    uint32_t pk[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pk[e] = pack2<T>(s[t4][8 * hh + 2 * e], s[t4][8 * hh + 2 * e + 1]);
+    const typename T::vec8 pb = __builtin_bit_cast(typename T::vec8, pk);
+    const int r1 = 16 * u + tr_row;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int x = 32 * dt + tr_col;
+      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) i16x4*)(sv16 + tile_elem<D>(r1, x)));
+      const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) i16x4*)(sv16 + tile_elem<D>(r1 + 8, x)));
+      const uint2 lo2 = __builtin_bit_cast(uint2, lo), hi2 = __builtin_bit_cast(uint2, hi);
+      const uint4 va = make_uint4(lo2.x, lo2.y, hi2.x, hi2.y);
+      st.o[dt] = T::mfma32(as_vec8<T>(va), pb, st.o[dt]);
+    }
+  }
+  lds_barrier();  // every wave is done with the V buffer
+  if (jn >= 0) issue_tile<D>(sv_w, vbase, vst, tv, jn, L, w, lane);
 }
 
 template <typename T, int D>
@@ -63,124 +259,55 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
   const int32_t* list = a.idx + row_tri;
   const int kvh = h / (a.Hq / a.Hkv);
 
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // wave index, kept in an SGPR
   const int half = lane >> 5, l32 = lane & 31;
   const int qrow = 32 * w + l32;           // query row inside the block
   const int qg = i * kBlock + qrow;         // query position inside the sequence
   const bool qvalid = qg < L;
   const float c = a.sm_scale_log2;
 
-  // Q^T as MFMA B operand: lane (query l32, dims 16 s + 8 half .. +7)
+  const uint16_t* kbase = a.k + t0 * a.kst + static_cast<int64_t>(kvh) * a.khs;
+  const uint16_t* vbase = a.v + t0 * a.vst + static_cast<int64_t>(kvh) * a.vhs;
+
+  // Q^T as MFMA B operand: lane (query l32, dims 16 s + 8 half .. +7); loaded
+  // before the first K/V tiles so the first K wait also covers it
   typename T::vec8 qb[KS];
   {
     const uint16_t* qp = a.q + (t0 + qg) * a.qst + static_cast<int64_t>(h) * a.qhs + 8 * half;
 #pragma unroll
     for (int s = 0; s < KS; ++s) qb[s] = as_vec8<T>(qvalid ? ld16(qp + 16 * s) : zero4());
   }
-
-  f32x16 o[DT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x16{};
-  float m_run = -INFINITY;
-  float l_part = half == 0 ? 1.0f : 0.0f;  // the two halves' partial sums add up to l
-
-  const uint16_t* kbase = a.k + t0 * a.kst + static_cast<int64_t>(kvh) * a.khs;
-  const uint16_t* vbase = a.v + t0 * a.vst + static_cast<int64_t>(kvh) * a.vhs;
-  const uint16_t* sv16 = reinterpret_cast<const uint16_t*>(sv);
-
-  // transposing-read coordinates of this lane (16-lane groups)
-  const int g16 = lane >> 4, i16 = lane & 15;
-  const int tr_row = 4 * (g16 >> 1) + (i16 >> 2);       // + 16 u (+ 8)
-  const int tr_col = 16 * (g16 & 1) + 4 * (i16 & 3);    // + 32 dt
-
-  for (int n = 0; n < ncnt; ++n) {
-    const int j = min(max(__builtin_amdgcn_readfirstlane(list[n]), 0), i);
-    __syncthreads();  // previous block's LDS reads are done
-    for (int cidx = t; cidx < kBlock * CH; cidx += 256) {
-      const int r = cidx / CH, ch = cidx % CH;
-      const int gk = j * kBlock + r;
-      uint4 kv = zero4(), vv = zero4();
-      if (gk < L) {
-        kv = ld16(kbase + static_cast<int64_t>(gk) * a.kst + 8 * ch);
-        vv = ld16(vbase + static_cast<int64_t>(gk) * a.vst + 8 * ch);
-      }
-      const int pos = r * CH + (ch ^ swz(r));
-      sk[pos] = kv;
-      sv[pos] = vv;
-    }
-    __syncthreads();
-
-    // S^T = K . Q^T: s[st][v] is key 32 st + 8 (v/4) + 4 half + v%4, query l32
-    f32x16 s[4];
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      s[st] = f32x16{};
-      const int r = 32 * st + l32;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const uint4 kop = sk[r * CH + ((2 * ks + half) ^ swz(r))];
-        s[st] = T::mfma32(as_vec8<T>(kop), qb[ks], s[st]);
-      }
-    }
-    if (j == i) {  // diagonal block: key > query is masked
-#pragma unroll
-      for (int st = 0; st < 4; ++st)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int key = 32 * st + 8 * (v >> 2) + 4 * half + (v & 3);
-          if (key > qrow) s[st][v] = -INFINITY;
-        }
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int st = 0; st < 4; ++st)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[st][v]);
-    mx = fmaxf(mx, xor32_f(mx));
-    const float m_new = fmaxf(m_run, mx * c);
-    float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    if (alpha != alpha) alpha = 1.0f;
-    float psum = 0.0f;
-#pragma unroll
-    for (int st = 0; st < 4; ++st)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(s[st][v], c, -m_new));
-        s[st][v] = p;
-        psum += p;
-      }
-    l_part = l_part * alpha + psum;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) o[dt][v] *= alpha;
-    m_run = m_new;
-
-    // O^T += V^T . P^T over 8 steps of 16 keys. B element e of lane (q, half)
-    // is key 16 u + (e < 4 ? 4 half + e : 8 + 4 half + e - 4); the A operand
-    // (V^T) is read in the same key order with two transposing reads.
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int st = u >> 1, hh = u & 1;
-      uint16_t pk[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pk[e] = T::from_f32(s[st][8 * hh + e]);
-      const typename T::vec8 pb = __builtin_bit_cast(typename T::vec8, pk);
-      const int r1 = 16 * u + tr_row;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const int x = 32 * dt + tr_col;
-        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) i16x4*)(sv16 + tile_elem<D>(r1, x)));
-        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) i16x4*)(sv16 + tile_elem<D>(r1 + 8, x)));
-        short va8[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        o[dt] = T::mfma32(__builtin_bit_cast(typename T::vec8, va8), pb, o[dt]);
-      }
-    }
+  TileLanes<D> tk, tv;
+  tk.init(a.kst, w, lane);
+  tv.init(a.vst, w, lane);
+  auto list_at = [&](int n) { return min(max(list[n], 0), i); };
+  if (ncnt > 0) {
+    const int j0 = list_at(0);
+    issue_tile<D>(sk, kbase, a.kst, tk, j0, L, w, lane);
+    issue_tile<D>(sv, vbase, a.vst, tv, j0, L, w, lane);
   }
 
-  const float l = l_part + xor32_f(l_part);
+  AttnState<T, D> st;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) st.o[dt] = f32x16{};
+  st.m_run = -INFINITY;
+  st.l_part = half == 0 ? 1.0f : 0.0f;  // the two halves' partial sums add up to l
+
+  const uint16_t* sv16 = reinterpret_cast<const uint16_t*>(sv);
+  // the diagonal block, when selected, is the last entry of the ascending list
+  const bool has_diag = ncnt > 0 && list_at(ncnt - 1) == i;
+  const int nplain = ncnt - (has_diag ? 1 : 0);
+  for (int n = 0; n < nplain; ++n) {
+    const int jn = n + 1 < ncnt ? list_at(n + 1) : -1;
+    attn_block<T, D, false>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv, jn, L,
+                            c, w, lane);
+  }
+  if (has_diag)
+    attn_block<T, D, true>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv, -1, L, c,
+                           w, lane);
+
+  const float l = st.l_part + xor32_f(st.l_part);
   const float rcp = 1.0f / l;
   if (qvalid) {
     uint16_t* op = a.o + (t0 + qg) * a.ost + static_cast<int64_t>(h) * a.ohs;
@@ -189,10 +316,10 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
         const int d = 32 * dt + 8 * g4 + 4 * half;
-        u16x4 pk;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) pk[r] = T::from_f32(o[dt][4 * g4 + r] * rcp);
-        *reinterpret_cast<u16x4*>(op + d) = pk;
+        uint2 pk;
+        pk.x = pack2<T>(st.o[dt][4 * g4 + 0] * rcp, st.o[dt][4 * g4 + 1] * rcp);
+        pk.y = pack2<T>(st.o[dt][4 * g4 + 2] * rcp, st.o[dt][4 * g4 + 3] * rcp);
+        *reinterpret_cast<uint2*>(op + d) = pk;
       }
   }
 }
