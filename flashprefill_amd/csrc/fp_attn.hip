@@ -70,9 +70,7 @@ __device__ __forceinline__ uint32_t pack2<F16>(float a, float b) {
 // wait for this wave's vector-memory ops down to N outstanding, then barrier
 template <int N>
 __device__ __forceinline__ void vm_barrier() {
-  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
-  else asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(N) : "memory");
 }
 // all of this wave's LDS reads are done, then barrier (buffer may be refilled)
 __device__ __forceinline__ void lds_barrier() {

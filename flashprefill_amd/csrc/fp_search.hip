@@ -82,11 +82,23 @@ __device__ void select_row(float* pl, const float* ml, int n, int i, int nb,
   if (t == 0) *count = running;
 }
 
+// LDS chunk swizzle of a 128 x D bf16 tile (16-byte chunks; conflict-free
+// MFMA A-operand reads of 16 rows x one chunk column on the 64-bank LDS)
+template <int D>
+__device__ __forceinline__ int qswz(int r) {
+  if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+  else return (r >> 1) & 7;
+}
+
+template <int D, bool FROM_SCORES>
+constexpr size_t search_q_bytes() { return FROM_SCORES ? 0 : kBlock * D * 2; }
+
 template <typename T, int D, bool FROM_SCORES>
-__global__ __launch_bounds__(256, 2) void k_search(SearchArgs a) {
-  extern __shared__ float dyn[];
-  float* pl = dyn;
-  float* ml = dyn + a.nb_max;
+__global__ __launch_bounds__(256, 3) void k_search(SearchArgs a) {
+  extern __shared__ uint4 dyn4[];
+  uint4* sq = dyn4;  // the query block (score mode only)
+  float* pl = reinterpret_cast<float*>(reinterpret_cast<char*>(dyn4) + search_q_bytes<D, FROM_SCORES>());
+  float* ml = pl + a.nb_max;
   int item, h;
   map_item(blockIdx.x, a.Hq, item, h);
   const int64_t nitems = a.tab.seq_tile[a.B];
@@ -112,17 +124,19 @@ __global__ __launch_bounds__(256, 2) void k_search(SearchArgs a) {
     const int kvh = h / (a.Hq / a.Hkv);
     const int half = lane >> 5, l32 = lane & 31;
     const float c = a.sm_scale_log2;
-    // Q block as MFMA A operands: rows 32*rg + l32, dims 16*s + 8*half .. +7
-    typename T::vec8 qa[4][KS];
-#pragma unroll
-    for (int rg = 0; rg < 4; ++rg) {
-      const int row = 32 * rg + l32;
-      const bool valid = i * kBlock + row < L;
-      const uint16_t* qp = a.q + (t0 + static_cast<int64_t>(i) * kBlock + row) * a.qst +
-                           static_cast<int64_t>(h) * a.qhs + 8 * half;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) qa[rg][s] = as_vec8<T>(valid ? ld16(qp + 16 * s) : zero4());
+    constexpr int CH = D / 8;
+    // stage the query block in LDS (rows past the sequence end are zero and
+    // still count for j < i); every wave reads it as MFMA A operands
+    // (rows 32*rg + l32, dims 16*s + 8*half .. +7)
+    for (int cidx = t; cidx < kBlock * CH; cidx += 256) {
+      const int r = cidx / CH, ch = cidx % CH;
+      uint4 val = zero4();
+      if (i * kBlock + r < L)
+        val = ld16(a.q + (t0 + static_cast<int64_t>(i) * kBlock + r) * a.qst +
+                   static_cast<int64_t>(h) * a.qhs + 8 * ch);
+      sq[r * CH + (ch ^ qswz<D>(r))] = val;
     }
+    __syncthreads();
     const int64_t mk_row = static_cast<int64_t>(a.Hkv) * D;
     const uint16_t* mkb = a.mk + tile_b * mk_row + static_cast<int64_t>(kvh) * D + 8 * half;
     const int ntiles = (n + 31) >> 5;
@@ -139,7 +153,11 @@ __global__ __launch_bounds__(256, 2) void k_search(SearchArgs a) {
 #pragma unroll
       for (int s = 0; s < KS; ++s)
 #pragma unroll
-        for (int rg = 0; rg < 4; ++rg) acc[rg] = T::mfma32(qa[rg][s], kb[s], acc[rg]);
+        for (int rg = 0; rg < 4; ++rg) {
+          const int r = 32 * rg + l32;
+          const uint4 qop = sq[r * CH + ((2 * s + half) ^ qswz<D>(r))];
+          acc[rg] = T::mfma32(as_vec8<T>(qop), kb[s], acc[rg]);
+        }
 
       // acc[rg][v] = Q[32 rg + 8 (v/4) + 4 half + v%4] . mk[j]
       float mx = -INFINITY, sum = 0.0f, m;
@@ -193,7 +211,8 @@ __global__ __launch_bounds__(256, 2) void k_search(SearchArgs a) {
 
 template <typename T, int D, bool FROM_SCORES>
 hipError_t launch_search_t(const SearchArgs& a, int64_t grid, hipStream_t s) {
-  const size_t shm = 2 * sizeof(float) * static_cast<size_t>(a.nb_max);
+  const size_t shm = search_q_bytes<D, FROM_SCORES>() +
+                     2 * sizeof(float) * static_cast<size_t>(a.nb_max);
   if (shm > 48 * 1024) {
     const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_search<T, D, FROM_SCORES>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
