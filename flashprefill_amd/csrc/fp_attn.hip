@@ -33,100 +33,9 @@
 // l accumulates the fp32 p, P is rounded to the input dtype before P.V, the
 // diagonal block masks key > query, and O = acc * (1/l). The accumulator is
 // rescaled only when some row's max moved (alpha == 1 makes it a no-op).
-#include "fp_internal.h"
+#include "fp_attn_common.h"
 
 namespace fp {
-
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void gbl_void_t;
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-
-// chunk swizzle of row r in a 128 x D tile (D/8 chunks of 16 bytes per row)
-template <int D>
-__device__ __forceinline__ int swz(int r) {
-  if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
-  else return (r >> 1) & 7;
-}
-
-template <int D>
-__device__ __forceinline__ int tile_elem(int r, int x) {
-  return r * D + ((((x >> 3) ^ swz<D>(r))) << 3) + (x & 7);
-}
-
-// two fp32 -> packed pair of the input type (round to nearest even)
-template <typename T>
-__device__ __forceinline__ uint32_t pack2(float a, float b);
-template <>
-__device__ __forceinline__ uint32_t pack2<BF16>(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
-}
-template <>
-__device__ __forceinline__ uint32_t pack2<F16>(float a, float b) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
-}
-
-// wait for this wave's vector-memory ops down to N outstanding, then barrier
-template <int N>
-__device__ __forceinline__ void vm_barrier() {
-  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(N) : "memory");
-}
-// all of this wave's LDS reads are done, then barrier (buffer may be refilled)
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// Direct-to-LDS loads of one 128 x D tile (block j of a K or V head). Wave w
-// fills the 1 KB LDS slices w*NI .. w*NI+NI-1; in each slice lane l writes
-// physical chunk l % CH of row slice*RPW + l / CH, so it fetches logical
-// chunk (l % CH) ^ swz(row) of that row. Because swz(row) only depends on
-// (l / CH) and on q modulo a small period, the per-lane part of the source
-// address is a 32-bit byte offset from a small precomputed table and the rest
-// is a wave-uniform (scalar) base.
-template <int D>
-struct TileLanes {
-  static constexpr int CH = D / 8;      // chunks per row
-  static constexpr int RPW = 64 / CH;   // rows per wave instruction
-  static constexpr int NI = CH / 2;     // instructions per wave per tile
-  static constexpr int PER = D == 128 ? 4 : 2;  // period of swz over q
-  uint32_t off[PER];                    // per-lane byte offsets
-  __device__ __forceinline__ void init(int64_t stride, int w, int lane) {
-#pragma unroll
-    for (int q = 0; q < PER; ++q) {
-      const int r = (w * NI + q) * RPW + lane / CH;
-      const int c = (lane % CH) ^ swz<D>(r);
-      off[q] = static_cast<uint32_t>(((lane / CH) * stride + 8 * c) * 2);
-    }
-  }
-};
-
-template <int D>
-__device__ __forceinline__ void issue_tile(uint4* lds, const uint16_t* base, int64_t stride,
-                                           const TileLanes<D>& tl, int j, int L, int w,
-                                           int lane) {
-  constexpr int CH = TileLanes<D>::CH, RPW = TileLanes<D>::RPW, NI = TileLanes<D>::NI;
-  if ((j + 1) * kBlock <= L) {
-#pragma unroll
-    for (int q = 0; q < NI; ++q) {
-      const int slot = w * NI + q;
-      const char* sbase = reinterpret_cast<const char*>(base) +
-                          static_cast<int64_t>(j * kBlock + slot * RPW) * stride * 2;
-      const char* src = sbase + tl.off[q % TileLanes<D>::PER];
-      __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)(lds + slot * 64), 16, 0, 0);
-    }
-  } else {  // partial last block: rows past the end read row L-1 (masked keys, p = 0)
-#pragma unroll
-    for (int q = 0; q < NI; ++q) {
-      const int slot = w * NI + q;
-      const int r = slot * RPW + lane / CH;
-      const int c = (lane % CH) ^ swz<D>(r);
-      const int gk = min(j * kBlock + r, L - 1);
-      const uint16_t* src = base + static_cast<int64_t>(gk) * stride + 8 * c;
-      __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)(lds + slot * 64), 16, 0, 0);
-    }
-  }
-}
 
 template <typename T, int D>
 struct AttnState {
@@ -244,8 +153,8 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
   map_item(blockIdx.x, a.Hq, item, h);
   const int64_t nitems = a.tab.seq_tile[a.B];
   if (item >= nitems) return;
-  const int b = a.tab.items[2 * item];
-  const int i = a.tab.items[2 * item + 1];
+  const int b = a.tab.items[item].b;
+  const int i = a.tab.items[item].i;
   const int64_t tile_b = a.tab.seq_tile[b];
   const int L = a.tab.seq_len[b];
   const int64_t t0 = a.tab.seq_start[b];

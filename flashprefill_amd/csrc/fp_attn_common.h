@@ -1,0 +1,167 @@
+// Building blocks of the gfx950 attention kernels: LDS tile layout (64-bank
+// chunk swizzle), direct-to-LDS tile loads, packed conversions and the
+// explicit wait + barrier helpers used to pipeline tile loads against MFMA.
+#pragma once
+
+#include "fp_internal.h"
+
+namespace fp {
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void gbl_void_t;
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Load through the scalar cache: the address must be wave-uniform and the
+// data must not be written while the kernel runs (tables and index lists
+// written by earlier kernels of the stream).
+template <typename X>
+__device__ __forceinline__ X sld(const X* p) {
+  static_assert(sizeof(X) % 4 == 0, "scalar loads move whole dwords");
+  const __attribute__((address_space(4))) uint32_t* w =
+      reinterpret_cast<const __attribute__((address_space(4))) uint32_t*>(
+          reinterpret_cast<uintptr_t>(p));
+  uint32_t buf[sizeof(X) / 4];
+#pragma unroll
+  for (unsigned k = 0; k < sizeof(X) / 4; ++k) buf[k] = w[k];
+  X x;
+  __builtin_memcpy(&x, buf, sizeof(X));
+  return x;
+}
+
+// chunk swizzle of row r in a 128 x D tile (D/8 chunks of 16 bytes per row)
+template <int D>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+  else return (r >> 1) & 7;
+}
+
+template <int D>
+__device__ __forceinline__ int tile_elem(int r, int x) {
+  return r * D + ((((x >> 3) ^ swz<D>(r))) << 3) + (x & 7);
+}
+
+// two fp32 -> packed pair of the input type (round to nearest even)
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float a, float b);
+template <>
+__device__ __forceinline__ uint32_t pack2<BF16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<F16>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+}
+
+// wait for this wave's vector-memory ops down to N outstanding, then barrier
+template <int N>
+__device__ __forceinline__ void vm_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" :: "n"(N) : "memory");
+}
+// all of this wave's LDS reads are done, then barrier (buffer may be refilled)
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Direct-to-LDS loads of one 128 x D tile (block j of a K or V head). Wave w
+// fills the 1 KB LDS slices w*NI .. w*NI+NI-1; in each slice lane l writes
+// physical chunk l % CH of row slice*RPW + l / CH, so it fetches logical
+// chunk (l % CH) ^ swz(row) of that row. Because swz(row) only depends on
+// (l / CH) and on q modulo a small period, the per-lane part of the source
+// address is a 32-bit byte offset from a small precomputed table and the rest
+// is a wave-uniform (scalar) base.
+template <int D>
+struct TileLanes {
+  static constexpr int CH = D / 8;      // chunks per row
+  static constexpr int RPW = 64 / CH;   // rows per wave instruction
+  static constexpr int NI = CH / 2;     // instructions per wave per tile
+  static constexpr int PER = D == 128 ? 4 : 2;  // period of swz over q
+  uint32_t off[PER];                    // per-lane byte offsets
+  __device__ __forceinline__ void init(int64_t stride, int w, int lane) {
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int r = (w * NI + q) * RPW + lane / CH;
+      const int c = (lane % CH) ^ swz<D>(r);
+      off[q] = static_cast<uint32_t>(((lane / CH) * stride + 8 * c) * 2);
+    }
+  }
+};
+
+template <int D>
+__device__ __forceinline__ void issue_tile(uint4* lds, const uint16_t* base, int64_t stride,
+                                           const TileLanes<D>& tl, int j, int L, int w,
+                                           int lane) {
+  constexpr int CH = TileLanes<D>::CH, RPW = TileLanes<D>::RPW, NI = TileLanes<D>::NI;
+  if ((j + 1) * kBlock <= L) {
+#pragma unroll
+    for (int q = 0; q < NI; ++q) {
+      const int slot = w * NI + q;
+      const char* sbase = reinterpret_cast<const char*>(base) +
+                          static_cast<int64_t>(j * kBlock + slot * RPW) * stride * 2;
+      const char* src = sbase + tl.off[q % TileLanes<D>::PER];
+      __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)(lds + slot * 64), 16, 0, 0);
+    }
+  } else {  // partial last block: rows past the end read row L-1 (masked keys, p = 0)
+#pragma unroll
+    for (int q = 0; q < NI; ++q) {
+      const int slot = w * NI + q;
+      const int r = slot * RPW + lane / CH;
+      const int c = (lane % CH) ^ swz<D>(r);
+      const int gk = min(j * kBlock + r, L - 1);
+      const uint16_t* src = base + static_cast<int64_t>(gk) * stride + 8 * c;
+      __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)(lds + slot * 64), 16, 0, 0);
+    }
+  }
+}
+
+// Lane offsets and direct-to-LDS loads of a half tile (64 rows of a 128-row
+// block; 16 KB at d = 128): wave w fills 1 KB slices w*NI .. w*NI+NI-1.
+template <int D>
+struct HalfLanes {
+  static constexpr int CH = D / 8;
+  static constexpr int RPW = 64 / CH;             // rows per 1 KB slice
+  static constexpr int NI = CH / 4;               // slices per wave per half tile
+  static constexpr int PER = D == 128 ? 4 : 2;    // period of swz over the slice index
+  uint32_t off[PER];
+  __device__ __forceinline__ void init(int64_t stride, int w, int lane) {
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int r = (w * NI + q) * RPW + lane / CH;
+      const int c = (lane % CH) ^ swz<D>(r);
+      off[q] = static_cast<uint32_t>(((lane / CH) * stride + 8 * c) * 2);
+    }
+  }
+};
+
+template <int D>
+__device__ __forceinline__ void issue_half(uint4* lds, const uint16_t* base, int64_t stride,
+                                           const HalfLanes<D>& tl, int j, int hf, int L, int w,
+                                           int lane) {
+  constexpr int CH = HalfLanes<D>::CH, RPW = HalfLanes<D>::RPW, NI = HalfLanes<D>::NI;
+  const int row0 = j * kBlock + 64 * hf;
+  if (row0 + 64 <= L) {
+#pragma unroll
+    for (int q = 0; q < NI; ++q) {
+      const int slot = w * NI + q;
+      const char* sbase = reinterpret_cast<const char*>(base) +
+                          static_cast<int64_t>(row0 + slot * RPW) * stride * 2;
+      __builtin_amdgcn_global_load_lds((gbl_void_t*)(sbase + tl.off[q % HalfLanes<D>::PER]),
+                                       (lds_void_t*)(lds + slot * 64), 16, 0, 0);
+    }
+  } else {  // rows past the sequence end read row L-1 (masked keys, p = 0)
+#pragma unroll
+    for (int q = 0; q < NI; ++q) {
+      const int slot = w * NI + q;
+      const int r = slot * RPW + lane / CH;
+      const int c = (lane % CH) ^ swz<D>(r);
+      const int gk = min(row0 + r, L - 1);
+      __builtin_amdgcn_global_load_lds(
+          (gbl_void_t*)(base + static_cast<int64_t>(gk) * stride + 8 * c),
+          (lds_void_t*)(lds + slot * 64), 16, 0, 0);
+    }
+  }
+}
+
+}  // namespace fp

@@ -5,6 +5,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <string>
@@ -65,6 +66,9 @@ int validate(const fp_problem* p) {
   for (int s = 0; s < 8; ++s)
     if (strides[s] < 0 || strides[s] % 8)
       return fail(FP_E_INVALID_ARG, "strides must be non-negative multiples of 8 elements");
+  for (int s = 0; s < 8; ++s)
+    if (strides[s] >= (int64_t(1) << 31))
+      return fail(FP_E_UNSUPPORTED, "strides of 2^31 elements or more are not supported");
   if (p->min_budget < 0) return fail(FP_E_INVALID_ARG, "min_budget < 0");
   if (p->min_budget > 0)
     return fail(FP_E_UNSUPPORTED, "min_budget > 0 is not implemented on the GPU path");
@@ -95,12 +99,39 @@ int layout(const fp_problem* p, fp_ws_layout* L) {
   L->seq_tri_off = off;    off = align_up(off + 8 * (B + 1));
   L->seq_start_off = off;  off = align_up(off + 8 * B);
   L->seq_len_off = off;    off = align_up(off + 4 * B);
-  L->items_off = off;      off = align_up(off + 8 * cap);
+  L->items_off = off;      off = align_up(off + sizeof(fp::ItemRec) * cap);
+  L->sched_off = off;      off = align_up(off + 4 * 16);
   L->mk_off = off;         off = align_up(off + 2 * cap * Hkv * d);
   L->cnt_off = off;        off = align_up(off + 4 * Hq * cap);
   L->idx_off = off;        off = align_up(off + 4 * Hq * tri);
   L->total_bytes = off;
   return FP_OK;
+}
+
+// Attention kernel choice, read at every call: the one-workgroup-per-row
+// kernel (default) or the persistent two-group kernel
+// (FLASHPREFILL_ATTN=persistent).
+int attn_impl() {
+  const char* e = getenv("FLASHPREFILL_ATTN");
+  return (e && strcmp(e, "persistent") == 0) ? 2 : 1;
+}
+
+// Workgroups of the persistent kernel: one per CU, a multiple of the 8 XCDs.
+hipError_t device_cus(int* out) {
+  static int cache[64] = {0};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  if (cache[dev] == 0) {
+    int n = 0;
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    n = (n / 8) * 8;
+    cache[dev] = n < 8 ? 8 : n;
+  }
+  *out = cache[dev];
+  return hipSuccess;
 }
 
 fp::SeqTables tables(const fp_ws_layout& L, void* ws) {
@@ -111,7 +142,7 @@ fp::SeqTables tables(const fp_ws_layout& L, void* ws) {
   t.seq_tri = reinterpret_cast<int64_t*>(base + L.seq_tri_off);
   t.seq_start = reinterpret_cast<int64_t*>(base + L.seq_start_off);
   t.seq_len = reinterpret_cast<int32_t*>(base + L.seq_len_off);
-  t.items = reinterpret_cast<int32_t*>(base + L.items_off);
+  t.items = reinterpret_cast<fp::ItemRec*>(base + L.items_off);
   return t;
 }
 
@@ -140,6 +171,7 @@ int run_plan(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   a.max_seq_len = p->max_seq_len;
   a.nb_max = L.nb_max;
   a.total_tokens = p->total_tokens;
+  a.sched = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + L.sched_off);
   const hipError_t e = fp::launch_plan(a, s);
   return e == hipSuccess ? FP_OK : hip_fail(e, "plan launch");
 }
@@ -199,6 +231,7 @@ int run_search(const fp_problem* p, const fp_ws_layout& L, void* ws, float* dp, 
 }
 
 int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s) {
+  if (p->total_tokens == 0) return FP_OK;  // no rows; the kernels assume a non-empty K
   fp::AttnArgs a;
   char* base = static_cast<char*>(ws);
   a.tab = tables(L, ws);
@@ -222,8 +255,16 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   a.Hq = p->num_q_heads;
   a.Hkv = p->num_kv_heads;
   a.sm_scale_log2 = sm_scale_log2(p->head_dim);
-  const hipError_t e = fp::launch_attn(a, p->dtype, p->head_dim,
-                                       static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap, s);
+  a.sched = reinterpret_cast<int32_t*>(base + L.sched_off);
+  hipError_t e;
+  if (attn_impl() == 1) {
+    e = fp::launch_attn(a, p->dtype, p->head_dim,
+                        static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap, s);
+  } else {
+    int cus = 0;
+    e = device_cus(&cus);
+    if (e == hipSuccess) e = fp::launch_attn_pp(a, p->dtype, p->head_dim, cus, s);
+  }
   return e == hipSuccess ? FP_OK : hip_fail(e, "attention launch");
 }
 
@@ -231,7 +272,7 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
 
 extern "C" {
 
-int fp_abi_version(void) { return 1; }
+int fp_abi_version(void) { return 2; }
 
 const char* fp_last_error(void) { return g_last_error.c_str(); }
 

@@ -135,6 +135,16 @@ __device__ __forceinline__ void map_item(int w, int num_q_heads, int& item, int&
   }
 }
 
+// One work item as the plan kernel records it (32 bytes, read with one scalar
+// load by the persistent attention kernel).
+struct ItemRec {
+  int32_t b, i;  // sequence, q-block
+  int32_t L;     // tokens of sequence b
+  int32_t tile;  // seq_tile[b] + i: the item's row in the per-block count table
+  int64_t t0;    // seq_start[b]
+  int64_t tri;   // seq_tri[b] + i (i + 1) / 2: start of the item's index list
+};
+
 // Workspace views shared by all kernels (device pointers into the workspace).
 struct SeqTables {
   uint32_t* status;
@@ -142,7 +152,7 @@ struct SeqTables {
   int64_t* seq_tri;    // [B+1] prefix of NB_b (NB_b + 1) / 2
   int64_t* seq_start;  // [B]   first token of sequence b
   int32_t* seq_len;    // [B]   tokens of sequence b (0 when skipped)
-  int32_t* items;      // [2 * nb_sum_cap] (b, i) heaviest first
+  ItemRec* items;      // [nb_sum_cap] work items, heaviest first
 };
 
 }  // namespace fp

@@ -9,6 +9,7 @@ namespace fp {
 
 struct PlanArgs {
   SeqTables tab;
+  int32_t* sched;     // attention work-queue counters (zeroed here)
   const int32_t* cu;  // nullable: uniform batch
   int32_t B;
   int32_t uniform_len;
@@ -56,6 +57,7 @@ struct AttnArgs {
   const int32_t* cnt;
   int64_t tri_cap;
   int64_t nb_sum_cap;
+  int32_t* sched;      // 8 per-XCD queue counters + 1 finish counter (persistent kernel)
   int32_t B, Hq, Hkv;
   float sm_scale_log2;
 };
@@ -65,5 +67,6 @@ hipError_t launch_pool(const PoolArgs& a, int dtype, int head_dim, int64_t grid,
 hipError_t launch_search(const SearchArgs& a, int dtype, int head_dim, int64_t grid,
                          bool from_scores, hipStream_t s);
 hipError_t launch_attn(const AttnArgs& a, int dtype, int head_dim, int64_t grid, hipStream_t s);
+hipError_t launch_attn_pp(const AttnArgs& a, int dtype, int head_dim, int num_wg, hipStream_t s);
 
 }  // namespace fp

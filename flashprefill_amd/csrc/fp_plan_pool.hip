@@ -48,6 +48,7 @@ __global__ __launch_bounds__(1024) void k_plan(PlanArgs a) {
   const int t = threadIdx.x, nt = blockDim.x;
   const SeqTables& tab = a.tab;
   if (t == 0) s_status = 0u;
+  if (t < 16) a.sched[t] = 0;
   __syncthreads();
 
   // 1. per-sequence lengths and validity
@@ -116,7 +117,8 @@ __global__ __launch_bounds__(1024) void k_plan(PlanArgs a) {
     }
   }
 
-  // 4. scatter (b, i) items: position = level offset + arrival order
+  // 4. scatter the item records: position = level offset + arrival order
+  //    (seq_len / seq_start / seq_tri were written above by this workgroup)
   const int nsum = s_pre[a.B];
   for (int g = t; g < nsum; g += nt) {
     int lo = 0, hi = a.B - 1;  // last b with s_pre[b] <= g
@@ -126,8 +128,14 @@ __global__ __launch_bounds__(1024) void k_plan(PlanArgs a) {
     }
     const int i = g - s_pre[lo];
     const int pos = atomicAdd(&s_lvl[i], 1);
-    tab.items[2 * pos] = lo;
-    tab.items[2 * pos + 1] = i;
+    ItemRec r;
+    r.b = lo;
+    r.i = i;
+    r.L = tab.seq_len[lo];
+    r.tile = g;
+    r.t0 = tab.seq_start[lo];
+    r.tri = tab.seq_tri[lo] + static_cast<int64_t>(i) * (i + 1) / 2;
+    tab.items[pos] = r;
   }
   __syncthreads();
   if (t == 0) *tab.status = s_status;

@@ -103,8 +103,8 @@ __global__ __launch_bounds__(256, 3) void k_search(SearchArgs a) {
   map_item(blockIdx.x, a.Hq, item, h);
   const int64_t nitems = a.tab.seq_tile[a.B];
   if (item >= nitems) return;
-  const int b = a.tab.items[2 * item];
-  const int i = a.tab.items[2 * item + 1];
+  const int b = a.tab.items[item].b;
+  const int i = a.tab.items[item].i;
   const int64_t tile_b = a.tab.seq_tile[b];
   const int nb = static_cast<int>(a.tab.seq_tile[b + 1] - tile_b);
   const int L = a.tab.seq_len[b];

@@ -18,6 +18,14 @@ _DTYPES = {torch.bfloat16: _lib.FP_DTYPE_BF16, torch.float16: _lib.FP_DTYPE_F16}
 BLOCK = 128
 
 
+def attn_key_tile() -> int:
+    """Keys per online-softmax step of the attention kernel the library runs:
+    128 for the one-workgroup-per-row kernel (default), 64 for the persistent
+    kernel selected with FLASHPREFILL_ATTN=persistent."""
+    import os
+    return 64 if os.environ.get("FLASHPREFILL_ATTN") == "persistent" else 128
+
+
 def _dtype_code(t: torch.Tensor) -> int:
     if t.dtype not in _DTYPES:
         raise NotImplementedError(
@@ -149,7 +157,7 @@ class FlashPrefillCall:
 
     def items(self) -> torch.Tensor:
         tile, _, _, _ = self.seq_tables()
-        return self._view(self.layout.items_off, torch.int32, 2 * tile[-1]).view(-1, 2)
+        return self._view(self.layout.items_off, torch.int32, 8 * tile[-1]).view(-1, 8)[:, :2]
 
     def pooled_k(self) -> torch.Tensor:
         tile, _, _, _ = self.seq_tables()

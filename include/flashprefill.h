@@ -102,7 +102,10 @@ typedef struct fp_ws_layout {
     size_t seq_tri_off;  /* int64[batch+1] */
     size_t seq_start_off; /* int64[batch]: first token of each sequence */
     size_t seq_len_off;  /* int32[batch]: tokens (0 for a skipped sequence) */
-    size_t items_off;    /* int32[2 * nb_sum_cap]: (b, i) heaviest first */
+    size_t items_off;    /* nb_sum_cap records of 32 bytes, heaviest first:
+                            int32 b, i, seq_len, seq_tile[b] + i;
+                            int64 seq_start, seq_tri[b] + i (i + 1) / 2 */
+    size_t sched_off;    /* int32[16]: attention work-queue counters */
     size_t mk_off;
     size_t cnt_off;
     size_t idx_off;

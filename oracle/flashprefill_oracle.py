@@ -24,9 +24,10 @@ sizes), the oracle fixes one canonical arithmetic and says so:
   fp32 argument and rounded to fp32 (i.e. correctly rounded fp32 exp2);
 * row sums in the native normalisation: fp64 sum of the fp32 terms, rounded
   once to fp32 (order independent);
-* attention: the online softmax is run block by block (one 128-key tile per
-  selected block), P is rounded to V's dtype before P@V, exactly as
-  ``…native_forward.py:311-331`` does for ``K_TILE_SIZE == BLOCK_SIZE``.
+* attention: the online softmax runs over key tiles of ``k_tile`` keys (128 by
+  default; 64 matches the reference's other autotuned K_TILE_SIZE and the GPU
+  persistent kernel), P is rounded to V's dtype before P@V, exactly as
+  ``…native_forward.py:298-331`` does.
 
 Pinning status (what checks each function, see ``tests/test_oracle.py``):
   pool_k            closed form (fp64 block mean) + mutation check
@@ -228,13 +229,14 @@ def select_from_scores(p: torch.Tensor, m: torch.Tensor, native: bool, alpha: fl
 # ---------------------------------------------------------------------------
 
 def sparse_attention(q_seq: torch.Tensor, k_seq: torch.Tensor, v_seq: torch.Tensor,
-                     sel: torch.Tensor, block: int = 128) -> torch.Tensor:
+                     sel: torch.Tensor, block: int = 128, k_tile: int = 128) -> torch.Tensor:
     """Online-softmax attention over the selected key blocks, in list order.
 
     Per (head h, q-block i) the selected blocks j are visited in ascending order
-    (:289-331). Inside a block: ``qk = Q K^T`` (fp32), the diagonal block masks
-    ``q_pos < k_pos`` to -inf (:312-315), ``qk *= sm_scale``; then
-    ``m_new = max(m, rowmax)``, ``p = exp2(qk - m_new)``,
+    (:289-331) and each block in key tiles of ``k_tile`` keys (the reference's
+    autotuned K_TILE_SIZE, 64 or 128, :298). Per tile: ``qk = Q K^T`` (fp32),
+    the diagonal block masks ``q_pos < k_pos`` to -inf (:312-315),
+    ``qk *= sm_scale``; then ``m_new = max(m, rowmax)``, ``p = exp2(qk - m_new)``,
     ``alpha = exp2(m - m_new)`` with NaN -> 1 (:323-325), ``l = l*alpha + sum p``,
     ``acc = acc*alpha + p.to(v.dtype) @ v`` (:326-330). ``m`` starts at -inf and
     ``l`` at 1.0 (:282-283). Output ``acc / l`` cast to q.dtype (:333-344).
@@ -246,6 +248,7 @@ def sparse_attention(q_seq: torch.Tensor, k_seq: torch.Tensor, v_seq: torch.Tens
     Hkv = k_seq.shape[1]
     G = Hq // Hkv
     nb = num_blocks(S, block)
+    assert block % k_tile == 0
     c = sm_scale_f32(d)
     pad = nb * block
     qf = torch.zeros(pad, Hq, d, dtype=torch.float64)
@@ -256,8 +259,7 @@ def sparse_attention(q_seq: torch.Tensor, k_seq: torch.Tensor, v_seq: torch.Tens
     vf[:S] = v_seq.float()
     out = torch.zeros(pad, Hq, d, dtype=torch.float32)
     ninf = torch.tensor(float("-inf"))
-    pos = torch.arange(block)
-    diag_mask = pos.view(block, 1) >= pos.view(1, block)  # q_pos >= k_pos
+    qpos = torch.arange(block).view(block, 1)
     for h in range(Hq):
         kvh = h // G
         for i in range(nb):
@@ -267,22 +269,24 @@ def sparse_attention(q_seq: torch.Tensor, k_seq: torch.Tensor, v_seq: torch.Tens
             l_i = torch.ones(block)
             acc = torch.zeros(block, d)
             for j in js:
-                kj = kf[j * block:(j + 1) * block, kvh, :]
-                vj = vf[j * block:(j + 1) * block, kvh, :]
-                qk = (qi @ kj.T).float()
-                if j == i:
-                    qk = torch.where(diag_mask, qk, ninf)
-                qk = qk * c
-                m_new = torch.maximum(m_i, qk.max(dim=1).values)
-                p = exp2_f32(qk - m_new.view(block, 1))
-                lij = p.double().sum(dim=1).float()
-                alpha = exp2_f32(m_i - m_new)
-                alpha = torch.where(torch.isnan(alpha), torch.ones(()), alpha)
-                acc = acc * alpha.view(block, 1)
-                l_i = l_i * alpha + lij
-                pv = p.to(v_seq.dtype).float()
-                acc = acc + (pv.double() @ vj.double()).float()
-                m_i = m_new
+                for k0 in range(j * block, (j + 1) * block, k_tile):
+                    kj = kf[k0:k0 + k_tile, kvh, :]
+                    vj = vf[k0:k0 + k_tile, kvh, :]
+                    qk = (qi @ kj.T).float()
+                    if j == i:
+                        kpos = torch.arange(k0 - j * block, k0 - j * block + k_tile).view(1, k_tile)
+                        qk = torch.where(qpos >= kpos, qk, ninf)
+                    qk = qk * c
+                    m_new = torch.maximum(m_i, qk.max(dim=1).values)
+                    p = exp2_f32(qk - m_new.view(block, 1))
+                    lij = p.double().sum(dim=1).float()
+                    alpha = exp2_f32(m_i - m_new)
+                    alpha = torch.where(torch.isnan(alpha), torch.ones(()), alpha)
+                    acc = acc * alpha.view(block, 1)
+                    l_i = l_i * alpha + lij
+                    pv = p.to(v_seq.dtype).float()
+                    acc = acc + (pv.double() @ vj.double()).float()
+                    m_i = m_new
             out[i * block:(i + 1) * block, h, :] = acc * (1.0 / l_i).view(block, 1)
     return out[:S].to(q_seq.dtype)
 

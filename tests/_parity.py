@@ -9,7 +9,7 @@ from typing import List, Optional, Sequence
 
 import torch
 
-from flashprefill_amd.runtime import FlashPrefillCall
+from flashprefill_amd.runtime import FlashPrefillCall, attn_key_tile
 from oracle import flashprefill_oracle as O
 
 OUT_MAX_ABS = 2e-2   # north-star output tolerance (bf16)
@@ -122,7 +122,8 @@ def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n
         for b, (s0, s1) in enumerate(seq_slices(cu_list)):
             if s1 == s0:
                 continue
-            ref = O.sparse_attention(q[s0:s1], k[s0:s1], v[s0:s1], gpu_sel[b])
+            ref = O.sparse_attention(q[s0:s1], k[s0:s1], v[s0:s1], gpu_sel[b],
+                                     k_tile=attn_key_tile())
             diffs.append((out[s0:s1].float() - ref.float()).abs().reshape(-1))
         d = torch.cat(diffs)
         assert not torch.isnan(d).any(), "NaN in GPU output"

@@ -20,6 +20,15 @@ from tests._parity import OUT_MAX_ABS, OUT_MEAN_ABS, run_stages
 
 pytestmark = pytest.mark.gpu
 
+# both attention kernels: one workgroup per row (default) and the persistent one
+KERNELS = ["rows", "persistent"]
+
+
+@pytest.fixture(params=KERNELS)
+def attn_kernel(request, monkeypatch):
+    monkeypatch.setenv("FLASHPREFILL_ATTN", request.param)
+    return request.param
+
 
 def _check(rep, max_flip_frac=2e-3):
     print(f"\n  pool_ulp={rep.pool_ulp} m_rel={rep.m_max_rel:.2e} p_rel={rep.p_max_rel:.2e} "
@@ -50,19 +59,19 @@ def _rand_inputs(lens, Hq, Hkv, d, dtype, seed, scale=1.0):
 
 
 @pytest.mark.parametrize("native", [False, True])
-def test_ragged_varlen_bf16(native):
+def test_ragged_varlen_bf16(native, attn_kernel):
     lens = [300, 128, 1, 640, 129]
     q, k, v, cu = _rand_inputs(lens, 8, 2, 128, torch.bfloat16, 1, scale=1.5)
     _check(run_stages(q, k, v, cu, max(lens), alpha=0.18, native=native))
 
 
-def test_llama_4k_structured():
+def test_llama_4k_structured(attn_kernel):
     spec = synth.llama_spec(4096, seed=4)
     q, k, v, cu = synth.make_inputs(spec)
     _check(run_stages(q, k, v, cu.tolist(), 4096, alpha=0.18))
 
 
-def test_qwen_heads_not_multiple_of_8_fp16_d64():
+def test_qwen_heads_not_multiple_of_8_fp16_d64(attn_kernel):
     lens = [1000, 555]
     q, k, v, cu = _rand_inputs(lens, 28, 4, 64, torch.float16, 2, scale=1.2)
     _check(run_stages(q, k, v, cu, 1000, alpha=0.08))

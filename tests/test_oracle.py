@@ -324,3 +324,15 @@ def test_rows_pipeline_equals_full_pipeline(native):
     for (h, i), (sel_row, o_row) in res.items():
         assert torch.equal(sel_row, tr.sel[h, i])
         assert torch.equal(o_row, out[i * 128:(i + 1) * 128, h])
+
+
+def test_sparse_attention_key_tile_64_matches_closed_form():
+    # the 64-key online-softmax tiling (the reference's other K_TILE_SIZE) is the same function
+    S, Hq, Hkv, d = 300, 2, 1, 16
+    q = _rand((S, Hq, d), 81, torch.float32, 1.5)
+    k = _rand((S, Hkv, d), 82, torch.float32, 1.5)
+    v = _rand((S, Hkv, d), 83)
+    sel = _random_sel(Hq, 3, 84)
+    got = O.sparse_attention(q, k, v, sel, k_tile=64).double()
+    ref = O.dense_masked_attention_fp64(q, k, v, sel)
+    assert (got - ref).abs().max().item() < 2e-5
