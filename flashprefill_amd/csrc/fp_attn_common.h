@@ -118,19 +118,22 @@ __device__ __forceinline__ void issue_tile(uint4* lds, const uint16_t* base, int
 
 // Lane offsets and direct-to-LDS loads of a half tile (64 rows of a 128-row
 // block; 16 KB at d = 128): wave w fills 1 KB slices w*NI .. w*NI+NI-1.
+// off[q] is this lane's byte offset from the half tile's first row for
+// slice w*NI + q, so every load of a tile uses one scalar base address
+// (64 * stride * 2 < 2^31 is checked on the host).
 template <int D>
 struct HalfLanes {
   static constexpr int CH = D / 8;
   static constexpr int RPW = 64 / CH;             // rows per 1 KB slice
   static constexpr int NI = CH / 4;               // slices per wave per half tile
   static constexpr int PER = D == 128 ? 4 : 2;    // period of swz over the slice index
-  uint32_t off[PER];
+  uint32_t off[NI];
   __device__ __forceinline__ void init(int64_t stride, int w, int lane) {
 #pragma unroll
-    for (int q = 0; q < PER; ++q) {
+    for (int q = 0; q < NI; ++q) {
       const int r = (w * NI + q) * RPW + lane / CH;
       const int c = (lane % CH) ^ swz<D>(r);
-      off[q] = static_cast<uint32_t>(((lane / CH) * stride + 8 * c) * 2);
+      off[q] = static_cast<uint32_t>((r * stride + 8 * c) * 2);
     }
   }
 };
@@ -142,12 +145,11 @@ __device__ __forceinline__ void issue_half(uint4* lds, const uint16_t* base, int
   constexpr int CH = HalfLanes<D>::CH, RPW = HalfLanes<D>::RPW, NI = HalfLanes<D>::NI;
   const int row0 = j * kBlock + 64 * hf;
   if (row0 + 64 <= L) {
+    const char* sbase = reinterpret_cast<const char*>(base) + static_cast<int64_t>(row0) * stride * 2;
 #pragma unroll
     for (int q = 0; q < NI; ++q) {
       const int slot = w * NI + q;
-      const char* sbase = reinterpret_cast<const char*>(base) +
-                          static_cast<int64_t>(row0 + slot * RPW) * stride * 2;
-      __builtin_amdgcn_global_load_lds((gbl_void_t*)(sbase + tl.off[q % HalfLanes<D>::PER]),
+      __builtin_amdgcn_global_load_lds((gbl_void_t*)(sbase + tl.off[q]),
                                        (lds_void_t*)(lds + slot * 64), 16, 0, 0);
     }
   } else {  // rows past the sequence end read row L-1 (masked keys, p = 0)
@@ -162,6 +164,22 @@ __device__ __forceinline__ void issue_half(uint4* lds, const uint16_t* base, int
           (lds_void_t*)(lds + slot * 64), 16, 0, 0);
     }
   }
+}
+
+// Reductions over the two 32-lane halves of a wave (lane l with l ^ 32):
+// v_permlane32_swap exchanges the halves of its two operands, so max / sum
+// of the pair it returns is the value of the two lanes, in every lane.
+__device__ __forceinline__ float pair32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
+                                                  __builtin_bit_cast(unsigned, x), false, false);
+  return fmaxf(__builtin_bit_cast(float, static_cast<unsigned>(r[0])),
+               __builtin_bit_cast(float, static_cast<unsigned>(r[1])));
+}
+__device__ __forceinline__ float pair32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
+                                                  __builtin_bit_cast(unsigned, x), false, false);
+  return __builtin_bit_cast(float, static_cast<unsigned>(r[0])) +
+         __builtin_bit_cast(float, static_cast<unsigned>(r[1]));
 }
 
 }  // namespace fp

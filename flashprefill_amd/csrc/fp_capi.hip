@@ -67,8 +67,8 @@ int validate(const fp_problem* p) {
     if (strides[s] < 0 || strides[s] % 8)
       return fail(FP_E_INVALID_ARG, "strides must be non-negative multiples of 8 elements");
   for (int s = 0; s < 8; ++s)
-    if (strides[s] >= (int64_t(1) << 31))
-      return fail(FP_E_UNSUPPORTED, "strides of 2^31 elements or more are not supported");
+    if (strides[s] >= (int64_t(1) << 24))
+      return fail(FP_E_UNSUPPORTED, "strides of 2^24 elements or more are not supported");
   if (p->min_budget < 0) return fail(FP_E_INVALID_ARG, "min_budget < 0");
   if (p->min_budget > 0)
     return fail(FP_E_UNSUPPORTED, "min_budget > 0 is not implemented on the GPU path");
@@ -93,6 +93,8 @@ int layout(const fp_problem* p, fp_ws_layout* L) {
   L->tri_cap = tri;
   const int64_t Hq = p->num_q_heads, Hkv = p->num_kv_heads, d = p->head_dim;
   if (Hq * cap > (int64_t(1) << 31)) return fail(FP_E_INVALID_ARG, "too many work items");
+  if (Hq * tri >= (int64_t(1) << 31))
+    return fail(FP_E_UNSUPPORTED, "index lists of 2^31 entries or more are not supported");
   size_t off = 0;
   L->status_off = off;     off = align_up(off + 4);
   L->seq_tile_off = off;   off = align_up(off + 8 * (B + 1));
