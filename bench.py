@@ -40,6 +40,12 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="time budget of the CPU baseline sample")
+    ap.add_argument("--collect-traffic", action="store_true",
+                    help="measure the attention kernel's HBM bytes per launch with two "
+                         "rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE), calibrated on a "
+                         "copy kernel, and write the summary under profiles/")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help=argparse.SUPPRESS)  # child of --collect-traffic: one attention + one copy
     return ap.parse_args()
 
 
@@ -57,6 +63,90 @@ def timed(fn, reps, stream=None):
     return s.elapsed_time(e) / reps
 
 
+COPY_BYTES = 1 << 30  # calibration copy: 1 GiB read + 1 GiB written
+
+
+def attn_kernel_name():
+    return "k_attn_pp" if os.environ.get("FLASHPREFILL_ATTN") == "persistent" else "k_attn"
+
+
+def traffic_file(S):
+    return os.path.join(ROOT, "profiles", f"attn_traffic_llama{S // 1024}k_{attn_kernel_name()}.json")
+
+
+def traffic_probe(args):
+    """One attention launch on the bench input and one plain 1 GiB copy, for
+    the counter passes of --collect-traffic."""
+    import torch
+    from flashprefill_amd import synth
+    from flashprefill_amd.runtime import FlashPrefillCall
+    dev = torch.device("cuda:0")
+    spec = synth.llama_spec(args.seq_len, seed=args.seed)
+    q, k, v, cu = synth.make_inputs(spec, device=dev)
+    o = torch.empty_like(q)
+    call = FlashPrefillCall(q, k, v, o, cu, args.seq_len, alpha=args.alpha)
+    call.plan(); call.pool(); call.search()
+    call.attn()
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    print("traffic probe done", flush=True)
+
+
+def collect_traffic(args):
+    """Two rocprofv3 counter passes over --traffic-probe (started as child
+    processes; this process never touches the GPU). FETCH_SIZE / WRITE_SIZE
+    of the attention dispatch are scaled by (known bytes / counter reading)
+    of the copy kernel in the same pass."""
+    import csv
+    import glob
+    import subprocess
+    import tempfile
+    probe = [sys.executable, "-u", os.path.abspath(__file__), "--traffic-probe",
+             "--seq-len", str(args.seq_len), "--seed", str(args.seed), "--alpha", str(args.alpha)]
+    res = {}
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        with tempfile.TemporaryDirectory() as td:
+            cmd = ["rocprofv3", "--pmc", ctr, "--output-format", "csv", "-d", td, "-o", "p", "--"] + probe
+            print("bench: " + " ".join(cmd), file=sys.stderr, flush=True)
+            r = subprocess.run(["timeout", "-s", "KILL", "300"] + cmd, capture_output=True, text=True)
+            if r.returncode != 0:
+                raise SystemExit(f"rocprofv3 pass {ctr} failed ({r.returncode}): {r.stderr[-800:]}")
+            vals = {}
+            for f in glob.glob(f"{td}/**/*counter_collection.csv", recursive=True):
+                for row in csv.DictReader(open(f)):
+                    name = row["Kernel_Name"]
+                    key = ("attn" if f"fp::{attn_kernel_name()}<" in name else
+                           "copy" if "copy" in name.lower() else None)
+                    if key is None or row["Counter_Name"] != ctr:
+                        continue
+                    vals.setdefault(key, []).append(float(row["Counter_Value"]))
+            if "attn" not in vals or "copy" not in vals:
+                raise SystemExit(f"counter {ctr}: dispatches not found ({sorted(vals)})")
+            # FETCH_SIZE / WRITE_SIZE are in KiB per dispatch; take the largest
+            # copy dispatch (the 1 GiB one)
+            attn_kib = vals["attn"][-1]
+            copy_kib = max(vals["copy"])
+            scale = COPY_BYTES / (copy_kib * 1024.0)
+            res[ctr] = {"attn_kib": attn_kib, "copy_kib": copy_kib, "copy_scale": scale,
+                        "attn_bytes": attn_kib * 1024.0 * scale}
+    out = {
+        "kernel": attn_kernel_name(), "workload": f"bench.py config 3, seq_len {args.seq_len}, "
+        f"seed {args.seed}, alpha {args.alpha}",
+        "command": ("python bench.py --collect-traffic  (runs, per counter: rocprofv3 --pmc "
+                    "<FETCH_SIZE|WRITE_SIZE> --output-format csv -- python -u bench.py "
+                    "--traffic-probe)"),
+        "calibration": f"torch copy of {COPY_BYTES} bytes in the same pass",
+        "fetch": res["FETCH_SIZE"], "write": res["WRITE_SIZE"],
+        "traffic_bytes": res["FETCH_SIZE"]["attn_bytes"] + res["WRITE_SIZE"]["attn_bytes"],
+    }
+    os.makedirs(os.path.dirname(traffic_file(args.seq_len)), exist_ok=True)
+    with open(traffic_file(args.seq_len), "w") as fh:
+        json.dump(out, fh, indent=1)
+    print(json.dumps(out), flush=True)
+
+
 def dense_causal_flops(S, Hq, d):
     return 2.0 * d * Hq * S * (S + 1)
 
@@ -64,7 +154,7 @@ def dense_causal_flops(S, Hq, d):
 def cpu_baseline(q, k, v, alpha, budget_s):
     """The oracle (a CPU restatement of the reference algorithm) on a bounded
     sample of the same workload: every query head, q-blocks visited from the
-    last one down in strides of 64, until ``budget_s`` seconds are used.
+    last one down in strides of 32, until ``budget_s`` seconds are used.
     Rate = dense-causal FLOPs of the sampled rows / CPU time (same unit as
     ``value``)."""
     import torch
@@ -76,7 +166,7 @@ def cpu_baseline(q, k, v, alpha, budget_s):
     t0 = time.perf_counter()
     mk = O.pool_k(kc)
     rows_done, flops = 0, 0.0
-    stride_rows = [i for i in range(nb - 1, -1, -64)]
+    stride_rows = [i for i in range(nb - 1, -1, -32)]
     for i in stride_rows:
         rows = [(h, i) for h in range(Hq)]
         O.flashprefill_rows(qc, kc, vc, rows, alpha=alpha, attention_sink=2, window=4,
@@ -94,13 +184,19 @@ def cpu_baseline(q, k, v, alpha, budget_s):
         "kind": "port",
         "sample": (f"oracle (pool K of all {nb} blocks, then score+select+attention) on "
                    f"{rows_done} (head, q-block) rows of the same 128K input: all {Hq} heads x "
-                   f"q-blocks {nb - 1}, {nb - 65}, ... ; {el:.1f} s on "
+                   f"q-blocks {nb - 1}, {nb - 33}, ... ; {el:.1f} s on "
                    f"{platform.processor() or platform.machine()}, os.cpu_count()={os.cpu_count()}"),
     }
 
 
 def main():
     args = parse()
+    if args.collect_traffic:
+        collect_traffic(args)
+        return
+    if args.traffic_probe:
+        traffic_probe(args)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (one MI355X per box); "
               "--gpus N with N > 1 is not supported", file=sys.stderr)
@@ -183,6 +279,15 @@ def main():
         print("bench: CPU baseline (oracle sample)", file=sys.stderr, flush=True)
         cpu = cpu_baseline(q, k, v, args.alpha, args.cpu_seconds)
 
+    traffic, traffic_src = None, None
+    tf = traffic_file(S)
+    if os.path.exists(tf):
+        with open(tf) as fh:
+            tj = json.load(fh)
+        if tj.get("kernel") == attn_kernel_name() and str(S) in tj.get("workload", ""):
+            traffic = int(tj["traffic_bytes"])
+            traffic_src = os.path.relpath(tf, ROOT)
+
     line = {
         "metric": METRIC,
         "value": round(eff_tflops, 3),
@@ -210,10 +315,12 @@ def main():
         "executed_tflops": round(exec_tflops, 2),
         "search_algorithmic_GBps": round(search_gbps, 1),
         "dense": {k2: (round(v2, 4) if isinstance(v2, float) else v2) for k2, v2 in dense.items()},
-        "roofline": {"bound": "mfma", "kernel": "k_attn (block-sparse attention)",
+        "roofline": {"bound": "mfma", "kernel": f"fp::{attn_kernel_name()} (block-sparse attention)",
                      "achieved": round(exec_tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(exec_tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": traffic, "traffic_unit": "bytes per launch (HBM, calibrated "
+                     "FETCH_SIZE + WRITE_SIZE)", "traffic_source": traffic_src,
+                     "algorithmic_kv_bytes": n_exec * 2 * 128 * d * q.element_size()},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
