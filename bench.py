@@ -33,6 +33,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=3,
+                    help="3 (default): the bench line; 2 or 4: a report line for BASELINE "
+                         "config 2 (Llama shapes at 4K/16K/32K) or 4 (Qwen2.5 varlen ragged)")
     ap.add_argument("--seq-len", type=int, default=131072)
     ap.add_argument("--seed", type=int, default=128)
     ap.add_argument("--alpha", type=float, default=0.18)
@@ -189,6 +192,129 @@ def cpu_baseline(q, k, v, alpha, budget_s):
     }
 
 
+def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines):
+    """Time one operator configuration: full call, search stage, attention
+    stage (HIP events on the launch stream), density and the dense baselines
+    (this kernel with every causal block selected, torch SDPA flash per
+    sequence with the KV heads expanded)."""
+    import torch
+    from flashprefill_amd.runtime import FlashPrefillCall
+    T, Hq, d = q.shape
+    Hkv = k.shape[1]
+    S_max = max(seq_lens)
+    o = torch.empty_like(q)
+    call = FlashPrefillCall(q, k, v, o, cu, S_max, alpha=alpha, attention_sink=2,
+                            window_size=4, last_n_block=2)
+    for _ in range(warmup):
+        call.run()
+    torch.cuda.synchronize()
+    print("bench: timing", file=sys.stderr, flush=True)
+    ms_total = timed(call.run, steps)
+
+    def search_stage():
+        call.plan()
+        call.pool()
+        call.search()
+
+    ms_search = timed(search_stage, max(3, steps))
+    ms_attn = timed(call.attn, max(3, steps))
+    assert call.status() == 0
+    tile, _, _, _ = call.seq_tables()
+    n_exec = int(call.counts()[:, :tile[-1]].sum().item())
+    causal_blocks = sum(Hq * ((s + 127) // 128) * ((s + 127) // 128 + 1) // 2 for s in seq_lens)
+    exec_tflops = 4.0 * 128 * 128 * d * n_exec / (ms_attn * 1e-3) / 1e12
+    dense_flops = sum(dense_causal_flops(s, Hq, d) for s in seq_lens)
+    out = {
+        "ms_total": ms_total, "ms_search": ms_search, "ms_attn": ms_attn,
+        "search_share": ms_search / ms_total, "executed_blocks": n_exec,
+        "density": n_exec / causal_blocks, "executed_tflops": exec_tflops,
+        "mfma_frac": exec_tflops / PEAK_BF16_TFLOPS,
+        "effective_tflops": dense_flops / (ms_total * 1e-3) / 1e12,
+        "search_algorithmic_GBps": (q.numel() + k.numel()) * q.element_size() /
+                                   (ms_search * 1e-3) / 1e9,
+        "dense": {},
+    }
+    if not dense_baselines:
+        return out
+    print("bench: dense baselines", file=sys.stderr, flush=True)
+    dense = out["dense"]
+    o2 = torch.empty_like(q)
+    dcall = FlashPrefillCall(q, k, v, o2, cu, S_max, alpha=0.0, attention_sink=2,
+                             window_size=4, last_n_block=2)
+    dcall.plan(); dcall.pool(); dcall.search()
+    dcall.attn()
+    dense["own_all_blocks_attn_ms"] = timed(dcall.attn, 1)
+    dense["own_all_blocks_tflops"] = dense_flops / (dense["own_all_blocks_attn_ms"] * 1e-3) / 1e12
+    del o2, dcall
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        offs = [0]
+        for s_ in seq_lens:
+            offs.append(offs[-1] + s_)
+        parts = []
+        for b in range(len(seq_lens)):
+            a0, a1 = offs[b], offs[b + 1]
+            parts.append((q[a0:a1].transpose(0, 1).unsqueeze(0),
+                          k[a0:a1].repeat_interleave(Hq // Hkv, dim=1).transpose(0, 1).unsqueeze(0),
+                          v[a0:a1].repeat_interleave(Hq // Hkv, dim=1).transpose(0, 1).unsqueeze(0)))
+
+        def sdpa_all():
+            for qh, kh, vh in parts:
+                torch.nn.functional.scaled_dot_product_attention(qh, kh, vh, is_causal=True)
+
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            sdpa_all()
+            dense["sdpa_flash_ms"] = timed(sdpa_all, 2)
+        dense["sdpa_flash_tflops"] = dense_flops / (dense["sdpa_flash_ms"] * 1e-3) / 1e12
+        del parts
+    except Exception as exc:  # the flash backend is the only one that fits long sequences
+        dense["sdpa_flash_error"] = f"{type(exc).__name__}: {exc}"[:200]
+    cands = [x for x in (dense.get("sdpa_flash_ms"), dense.get("own_all_blocks_attn_ms")) if x]
+    if cands:
+        dense["fastest_dense_ms"] = min(cands)
+        dense["speedup_vs_dense"] = min(cands) / ms_total
+    return out
+
+
+def _rounded(x):
+    if isinstance(x, float):
+        return round(x, 4)
+    if isinstance(x, dict):
+        return {k: _rounded(v) for k, v in x.items()}
+    return x
+
+
+def other_config(args):
+    """BASELINE configs 2 (Llama shapes at 4K / 16K / 32K) and 4 (Qwen2.5 varlen
+    ragged batch): one JSON report line, secondary to the config-3 bench line."""
+    import torch
+    from flashprefill_amd import synth
+    dev = torch.device("cuda:0")
+    results = []
+    if args.config == 2:
+        cases = [(synth.llama_spec(S, seed=seed), 0.18, f"{S // 1024}K")
+                 for S, seed in ((4096, 4), (16384, 16), (32768, 32))]
+    elif args.config == 4:
+        cases = [(synth.qwen_varlen_spec(), 0.08,
+                  "ragged {256K, 64K, 17K, 3K, 1K}, Qwen2.5-7B heads")]
+    else:
+        raise SystemExit(f"--config {args.config}: 2, 3 or 4")
+    for spec, alpha, name in cases:
+        print(f"bench: config {args.config} {name}", file=sys.stderr, flush=True)
+        q, k, v, cu = synth.make_inputs(spec, device=dev)
+        r = measure(q, k, v, cu, list(spec.seq_lens), alpha, args.steps, args.warmup,
+                    not args.no_dense)
+        r.update({"case": name, "seq_lens": list(spec.seq_lens), "num_q_heads": spec.num_q_heads,
+                  "num_kv_heads": spec.num_kv_heads, "head_dim": spec.head_dim, "alpha": alpha,
+                  "seed": spec.seed})
+        results.append(_rounded(r))
+        del q, k, v, cu
+        torch.cuda.empty_cache()
+    print(json.dumps({"report": f"BASELINE config {args.config}", "n_gpus": 1, "dtype": "bf16",
+                      "data": "synthetic (flashprefill_amd/synth.py)",
+                      "attention_kernel": attn_kernel_name(), "results": results}), flush=True)
+
+
 def main():
     args = parse()
     if args.collect_traffic:
@@ -203,76 +329,21 @@ def main():
         sys.exit(2)
     import torch
     from flashprefill_amd import synth
-    from flashprefill_amd.runtime import FlashPrefillCall
 
-    dev = torch.device("cuda:0")
+    if args.config != 3:
+        other_config(args)
+        return
     S = args.seq_len
     spec = synth.llama_spec(S, seed=args.seed)
-    print(f"bench: generating {S}-token structured input on {dev}", file=sys.stderr, flush=True)
-    q, k, v, cu = synth.make_inputs(spec, device=dev)
+    print(f"bench: generating {S}-token structured input on cuda:0", file=sys.stderr, flush=True)
+    q, k, v, cu = synth.make_inputs(spec, device=torch.device("cuda:0"))
     Hq, Hkv, d = spec.num_q_heads, spec.num_kv_heads, spec.head_dim
-    o = torch.empty_like(q)
-    call = FlashPrefillCall(q, k, v, o, cu, S, alpha=args.alpha, attention_sink=2,
-                            window_size=4, last_n_block=2)
-
-    for _ in range(args.warmup):
-        call.run()
-    torch.cuda.synchronize()
-    print("bench: timing", file=sys.stderr, flush=True)
-    ms_total = timed(call.run, args.steps)
-
-    def search_stage():
-        call.plan()
-        call.pool()
-        call.search()
-
-    ms_search = timed(search_stage, max(3, args.steps))
-    ms_attn = timed(call.attn, max(3, args.steps))
-    assert call.status() == 0
-
-    nb = (S + 127) // 128
-    tile, _, _, _ = call.seq_tables()
-    n_exec = int(call.counts()[:, :tile[-1]].sum().item())
-    causal_blocks = Hq * nb * (nb + 1) // 2
-    density = n_exec / causal_blocks
-    exec_flops = 4.0 * 128 * 128 * d * n_exec
-    dense_flops = dense_causal_flops(S, Hq, d)
-    exec_tflops = exec_flops / (ms_attn * 1e-3) / 1e12
-    eff_tflops = dense_flops / (ms_total * 1e-3) / 1e12
-    search_bytes = (q.numel() + k.numel()) * q.element_size()
-    search_gbps = search_bytes / (ms_search * 1e-3) / 1e9
-
-    dense = {}
-    if not args.no_dense:
-        print("bench: dense baselines", file=sys.stderr, flush=True)
-        # our own kernel with every causal block selected (alpha = 0 keeps S >= 0)
-        o2 = torch.empty_like(q)
-        dcall = FlashPrefillCall(q, k, v, o2, cu, S, alpha=0.0, attention_sink=2,
-                                 window_size=4, last_n_block=2)
-        dcall.plan(); dcall.pool(); dcall.search()
-        dcall.attn()
-        dense["own_all_blocks_attn_ms"] = timed(dcall.attn, 1)
-        dense["own_all_blocks_tflops"] = dense_flops / (dense["own_all_blocks_attn_ms"] * 1e-3) / 1e12
-        del o2, dcall
-        try:
-            from torch.nn.attention import SDPBackend, sdpa_kernel
-            qh = q.transpose(0, 1).unsqueeze(0)
-            kh = k.repeat_interleave(Hq // Hkv, dim=1).transpose(0, 1).unsqueeze(0)
-            vh = v.repeat_interleave(Hq // Hkv, dim=1).transpose(0, 1).unsqueeze(0)
-            with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
-                torch.nn.functional.scaled_dot_product_attention(qh, kh, vh, is_causal=True)
-                dense["sdpa_flash_ms"] = timed(
-                    lambda: torch.nn.functional.scaled_dot_product_attention(
-                        qh, kh, vh, is_causal=True), 2)
-            dense["sdpa_flash_tflops"] = dense_flops / (dense["sdpa_flash_ms"] * 1e-3) / 1e12
-            del qh, kh, vh
-        except Exception as exc:  # the flash backend is the only one that fits 128K
-            dense["sdpa_flash_error"] = f"{type(exc).__name__}: {exc}"[:200]
-        cands = [x for x in (dense.get("sdpa_flash_ms"), dense.get("own_all_blocks_attn_ms"))
-                 if x]
-        if cands:
-            dense["fastest_dense_ms"] = min(cands)
-            dense["speedup_vs_dense"] = min(cands) / ms_total
+    r = measure(q, k, v, cu, [S], args.alpha, args.steps, args.warmup, not args.no_dense)
+    ms_total, ms_search, ms_attn = r["ms_total"], r["ms_search"], r["ms_attn"]
+    n_exec, density, exec_tflops, eff_tflops = (r["executed_blocks"], r["density"],
+                                                r["executed_tflops"], r["effective_tflops"])
+    search_gbps = r["search_algorithmic_GBps"]
+    dense = r["dense"]
 
     cpu = None
     if not args.no_cpu:
