@@ -101,3 +101,19 @@ def test_check_maps_codes_to_python_exceptions():
     rc, _ = _layout(_problem(num_kv_heads=3))
     with pytest.raises(ValueError):
         _lib.check(rc)
+
+
+def test_ops_shim_exposes_the_reference_module_layout():
+    # the reference's callers import `from ops import ...` and
+    # `from ops.flashprefill_native_forward import flash_prefill`
+    import inspect
+    import ops
+    from ops.flashprefill_native_forward import flash_prefill
+    from ops.flashprefill_varlen_func import flash_prefill_varlen_func
+    import flashprefill_amd
+    assert ops.flash_prefill is flash_prefill is flashprefill_amd.flash_prefill
+    assert ops.flash_prefill_varlen_func is flash_prefill_varlen_func is \
+        flashprefill_amd.flash_prefill_varlen_func
+    assert list(inspect.signature(flash_prefill_varlen_func).parameters)[:11] == [
+        "q", "k", "v", "o", "cu_seqlens", "max_seq_len", "alpha", "block_size",
+        "attention_sink", "window_size", "last_n_block"]
