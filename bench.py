@@ -34,8 +34,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3,
-                    help="3 (default): the bench line; 2 or 4: a report line for BASELINE "
-                         "config 2 (Llama shapes at 4K/16K/32K) or 4 (Qwen2.5 varlen ragged)")
+                    help="3 (default): the bench line; 2, 4 or 5: a report line for BASELINE "
+                         "config 2 (Llama shapes at 4K/16K/32K), 4 (Qwen2.5 varlen ragged) or "
+                         "5 (64K decoder-layer attention block)")
     ap.add_argument("--seq-len", type=int, default=131072)
     ap.add_argument("--seed", type=int, default=128)
     ap.add_argument("--alpha", type=float, default=0.18)
@@ -291,6 +292,9 @@ def other_config(args):
     from flashprefill_amd import synth
     dev = torch.device("cuda:0")
     results = []
+    if args.config == 5:
+        print(json.dumps(decoder_layer_report(args)), flush=True)
+        return
     if args.config == 2:
         cases = [(synth.llama_spec(S, seed=seed), 0.18, f"{S // 1024}K")
                  for S, seed in ((4096, 4), (16384, 16), (32768, 32))]
@@ -298,7 +302,7 @@ def other_config(args):
         cases = [(synth.qwen_varlen_spec(), 0.08,
                   "ragged {256K, 64K, 17K, 3K, 1K}, Qwen2.5-7B heads")]
     else:
-        raise SystemExit(f"--config {args.config}: 2, 3 or 4")
+        raise SystemExit(f"--config {args.config}: 2, 3, 4 or 5")
     for spec, alpha, name in cases:
         print(f"bench: config {args.config} {name}", file=sys.stderr, flush=True)
         q, k, v, cu = synth.make_inputs(spec, device=dev)
@@ -313,6 +317,58 @@ def other_config(args):
     print(json.dumps({"report": f"BASELINE config {args.config}", "n_gpus": 1, "dtype": "bf16",
                       "data": "synthetic (flashprefill_amd/synth.py)",
                       "attention_kernel": attn_kernel_name(), "results": results}), flush=True)
+
+
+def decoder_layer_report(args):
+    """one prefill attention block at 64K tokens (hidden
+    4096, 32 q / 4 kv heads, d = 128, bf16, RoPE theta 1e6, random-init
+    weights, no q/k norm as in the BASELINE text): QKV projection -> RoPE ->
+    FlashPrefill (varlen signature, cu_seqlens = [0, S]) -> O projection."""
+    import torch
+    from flashprefill_amd import flash_prefill_varlen_func
+    from flashprefill_amd.attention_layer import PrefillAttention
+    from flashprefill_amd.runtime import FlashPrefillCall
+    dev = torch.device("cuda:0")
+    S, hidden, Hq, Hkv, d, alpha = 65536, 4096, 32, 4, 128, 0.12
+    layer = PrefillAttention(hidden, Hq, Hkv, d, rope_theta=1e6, alpha=alpha, device=dev, seed=5)
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(S, hidden, generator=g, device=dev).to(torch.bfloat16)
+    cu = torch.tensor([0, S], dtype=torch.int32, device=dev)
+    for _ in range(args.warmup):
+        layer(x, cu, S)
+    ms_layer = timed(lambda: layer(x, cu, S), args.steps)
+    ms_qkv = timed(lambda: layer.project_qkv(x, cu), args.steps)
+    q, k, v = layer.project_qkv(x, cu)
+    o = torch.empty_like(q)
+    ms_attn = timed(lambda: flash_prefill_varlen_func(q, k, v, o, cu, S, alpha), args.steps)
+    ms_oproj = timed(lambda: o.view(S, Hq * d) @ layer.w_o.t(), args.steps)
+    call = FlashPrefillCall(q, k, v, torch.empty_like(q), cu, S, alpha=alpha)
+    call.run()
+    torch.cuda.synchronize()
+    nb = S // 128
+    n_exec = int(call.counts()[:, :nb].sum().item())
+    density = n_exec / (Hq * nb * (nb + 1) // 2)
+    rep = {"report": "BASELINE config 5", "n_gpus": 1, "dtype": "bf16",
+           "data": "synthetic: hidden states ~ N(0,1), random-init weights (seed 5)",
+           "attention_kernel": attn_kernel_name(),
+           "config": {"seq_len": S, "hidden": hidden, "num_q_heads": Hq, "num_kv_heads": Hkv,
+                      "head_dim": d, "rope_theta": 1e6, "alpha": alpha, "qk_norm": False},
+           "ms_layer": ms_layer, "ms_qkv_proj_rope": ms_qkv, "ms_flashprefill": ms_attn,
+           "ms_o_proj": ms_oproj, "attention_share": ms_attn / ms_layer, "density": density,
+           "qkv_proj_tflops": 2.0 * S * hidden * (Hq + 2 * Hkv) * d / (ms_qkv * 1e-3) / 1e12}
+    if not args.no_dense:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        qh = q.transpose(0, 1).unsqueeze(0)
+        kh = k.repeat_interleave(Hq // Hkv, dim=1).transpose(0, 1).unsqueeze(0)
+        vh = v.repeat_interleave(Hq // Hkv, dim=1).transpose(0, 1).unsqueeze(0)
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            torch.nn.functional.scaled_dot_product_attention(qh, kh, vh, is_causal=True)
+            ms_dense = timed(lambda: torch.nn.functional.scaled_dot_product_attention(
+                qh, kh, vh, is_causal=True), 2)
+        rep["ms_dense_attention_sdpa_flash"] = ms_dense
+        rep["ms_layer_with_dense_attention"] = ms_layer - ms_attn + ms_dense
+        rep["layer_speedup_vs_dense"] = rep["ms_layer_with_dense_attention"] / ms_layer
+    return _rounded(rep)
 
 
 def main():
