@@ -65,6 +65,40 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Direct-to-LDS loads (global_load_lds_dwordx4: 64 lanes x 16 bytes into LDS
+// at M0 + 16 * lane) are issued from inline asm. The compiler models a
+// global_load_lds it generates as an LDS event of its own kind and, while one
+// is outstanding, turns every wait for an ordinary LDS read into lgkmcnt(0)
+// and every wait for a register load into vmcnt(0), which serialises the MFMA
+// operand reads. The attention kernels need no compiler tracking of these
+// loads: they wait for them explicitly (vmcnt at their barriers), and no
+// compiler-generated instruction in them uses M0. s_nop 4 gives the five wait
+// states a VMEM instruction needs after a VALU write of its SGPRs (the
+// readfirstlane of the base) and after the M0 write.
+__device__ __forceinline__ uint32_t lds_addr(void* p) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)p))));
+}
+// A wave-uniform 64-bit address as a scalar operand. readfirstlane returns
+// int: each half goes through uint32_t before widening (no sign extension).
+__device__ __forceinline__ uint64_t scalar_addr(const void* p) {
+  const uint64_t b = reinterpret_cast<uintptr_t>(p);
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b)));
+  const uint32_t hi =
+      static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+// one load: scalar base + 32-bit lane offset
+__device__ __forceinline__ void dma16_saddr(void* lds_slice, const void* base, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(lds_addr(lds_slice)), "v"(voff), "s"(scalar_addr(base)) : "memory", "m0");
+}
+// one load: per-lane 64-bit address
+__device__ __forceinline__ void dma16_vaddr(void* lds_slice, const void* src) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, off"
+               :: "s"(lds_addr(lds_slice)), "v"(src) : "memory", "m0");
+}
+
 // Direct-to-LDS loads of one 128 x D tile (block j of a K or V head). Wave w
 // fills the 1 KB LDS slices w*NI .. w*NI+NI-1; in each slice lane l writes
 // physical chunk l % CH of row slice*RPW + l / CH, so it fetches logical
@@ -100,8 +134,7 @@ __device__ __forceinline__ void issue_tile(uint4* lds, const uint16_t* base, int
       const int slot = w * NI + q;
       const char* sbase = reinterpret_cast<const char*>(base) +
                           static_cast<int64_t>(j * kBlock + slot * RPW) * stride * 2;
-      const char* src = sbase + tl.off[q % TileLanes<D>::PER];
-      __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)(lds + slot * 64), 16, 0, 0);
+      dma16_saddr(lds + slot * 64, sbase, tl.off[q % TileLanes<D>::PER]);
     }
   } else {  // partial last block: rows past the end read row L-1 (masked keys, p = 0)
 #pragma unroll
@@ -110,8 +143,7 @@ __device__ __forceinline__ void issue_tile(uint4* lds, const uint16_t* base, int
       const int r = slot * RPW + lane / CH;
       const int c = (lane % CH) ^ swz<D>(r);
       const int gk = min(j * kBlock + r, L - 1);
-      const uint16_t* src = base + static_cast<int64_t>(gk) * stride + 8 * c;
-      __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)(lds + slot * 64), 16, 0, 0);
+      dma16_vaddr(lds + slot * 64, base + static_cast<int64_t>(gk) * stride + 8 * c);
     }
   }
 }
@@ -149,8 +181,7 @@ __device__ __forceinline__ void issue_half(uint4* lds, const uint16_t* base, int
 #pragma unroll
     for (int q = 0; q < NI; ++q) {
       const int slot = w * NI + q;
-      __builtin_amdgcn_global_load_lds((gbl_void_t*)(sbase + tl.off[q]),
-                                       (lds_void_t*)(lds + slot * 64), 16, 0, 0);
+      dma16_saddr(lds + slot * 64, sbase, tl.off[q]);
     }
   } else {  // rows past the sequence end read row L-1 (masked keys, p = 0)
 #pragma unroll
@@ -159,9 +190,7 @@ __device__ __forceinline__ void issue_half(uint4* lds, const uint16_t* base, int
       const int r = slot * RPW + lane / CH;
       const int c = (lane % CH) ^ swz<D>(r);
       const int gk = min(row0 + r, L - 1);
-      __builtin_amdgcn_global_load_lds(
-          (gbl_void_t*)(base + static_cast<int64_t>(gk) * stride + 8 * c),
-          (lds_void_t*)(lds + slot * 64), 16, 0, 0);
+      dma16_vaddr(lds + slot * 64, base + static_cast<int64_t>(gk) * stride + 8 * c);
     }
   }
 }

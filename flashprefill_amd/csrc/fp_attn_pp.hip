@@ -80,34 +80,12 @@ using Parity = std::integral_constant<int, P>;
 
 constexpr int kRing = 8;  // row descriptors per group: positions t-1 .. t+3 span at most 5 rows
 
-// Direct-to-LDS loads are issued from inline asm. The compiler models a
-// global_load_lds it generates as an LDS event of its own kind and, while one
-// is outstanding, turns every wait for an ordinary LDS read into lgkmcnt(0),
-// which serialises the MFMA operand reads. These loads need no compiler
-// tracking: the kernel waits for them explicitly (vmcnt at the phase
-// barriers) and no compiler-generated instruction here uses M0.
-__device__ __forceinline__ uint32_t lds_addr(void* p) {
-  return __builtin_amdgcn_readfirstlane(
-      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void_t*)p)));
-}
-
 // One direct-to-LDS load (1 KB slice w*NI + q) of a full 64-row half tile:
 // 32-bit lane offset from a scalar base.
 template <int D>
 __device__ __forceinline__ void dma_slice(uint4* lds, const uint16_t* base,
                                           const HalfLanes<D>& tl, int q, int w) {
-  const uint32_t m0 = lds_addr(lds + (w * HalfLanes<D>::NI + q) * 64);
-  // the base is wave-uniform by construction; readfirstlane returns int, so
-  // each half goes through uint32_t before widening (no sign extension)
-  const uint64_t b = reinterpret_cast<uintptr_t>(base);
-  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b)));
-  const uint32_t hi =
-      static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)));
-  const uint64_t sb = (static_cast<uint64_t>(hi) << 32) | lo;
-  // s_nop 4: five wait states after the M0 write and after a VALU write of
-  // the base SGPRs (readfirstlane) before the load reads them
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, %2"
-               :: "s"(m0), "v"(tl.off[q]), "s"(sb) : "memory", "m0");
+  dma16_saddr(lds + (w * HalfLanes<D>::NI + q) * 64, base, tl.off[q]);
 }
 
 // All loads of a half tile with fewer than 64 rows inside the sequence: rows
@@ -122,10 +100,7 @@ __device__ __forceinline__ void dma_partial(uint4* lds, const uint16_t* base, in
     const int r = slot * RPW + lane / CH;
     const int c = (lane % CH) ^ swz<D>(r);
     const int gk = min(r, nvalid - 1);
-    const uint16_t* src = base + static_cast<int64_t>(gk) * stride + 8 * c;
-    const uint32_t m0 = lds_addr(lds + slot * 64);
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, off"
-                 :: "s"(m0), "v"(src) : "memory", "m0");
+    dma16_vaddr(lds + slot * 64, base + static_cast<int64_t>(gk) * stride + 8 * c);
   }
 }
 
