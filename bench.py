@@ -71,7 +71,8 @@ COPY_BYTES = 1 << 30  # calibration copy: 1 GiB read + 1 GiB written
 
 
 def attn_kernel_name():
-    return "k_attn_pp" if os.environ.get("FLASHPREFILL_ATTN") == "persistent" else "k_attn"
+    return {"persistent": "k_attn_pp", "wide": "k_attn_wide"}.get(
+        os.environ.get("FLASHPREFILL_ATTN", ""), "k_attn")
 
 
 def traffic_file(S):

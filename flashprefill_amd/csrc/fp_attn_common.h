@@ -98,6 +98,20 @@ __device__ __forceinline__ void dma16_vaddr(void* lds_slice, const void* src) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, off"
                :: "s"(lds_addr(lds_slice)), "v"(src) : "memory", "m0");
 }
+// the same two loads with the LDS slice given as a wave-uniform LDS byte address
+__device__ __forceinline__ void dma16_saddr_at(uint32_t lds, const void* base, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(lds), "v"(voff), "s"(scalar_addr(base)) : "memory", "m0");
+}
+// one load: an address already held in SGPRs + 32-bit lane offset
+__device__ __forceinline__ void dma16_sbase_at(uint32_t lds, uint64_t sbase, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(lds), "v"(voff), "s"(sbase) : "memory", "m0");
+}
+__device__ __forceinline__ void dma16_vaddr_at(uint32_t lds, const void* src) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, off"
+               :: "s"(lds), "v"(src) : "memory", "m0");
+}
 
 // Direct-to-LDS loads of one 128 x D tile (block j of a K or V head). Wave w
 // fills the 1 KB LDS slices w*NI .. w*NI+NI-1; in each slice lane l writes

@@ -111,11 +111,14 @@ int layout(const fp_problem* p, fp_ws_layout* L) {
 }
 
 // Attention kernel choice, read at every call: the one-workgroup-per-row
-// kernel (default) or the persistent two-group kernel
-// (FLASHPREFILL_ATTN=persistent).
+// kernel (default), the persistent two-group kernel
+// (FLASHPREFILL_ATTN=persistent) or the two-wave, 64-queries-per-wave row
+// kernel (FLASHPREFILL_ATTN=wide).
 int attn_impl() {
   const char* e = getenv("FLASHPREFILL_ATTN");
-  return (e && strcmp(e, "persistent") == 0) ? 2 : 1;
+  if (e && strcmp(e, "persistent") == 0) return 2;
+  if (e && strcmp(e, "wide") == 0) return 3;
+  return 1;
 }
 
 // Workgroups of the persistent kernel: one per CU, a multiple of the 8 XCDs.
@@ -259,9 +262,13 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   a.sm_scale_log2 = sm_scale_log2(p->head_dim);
   a.sched = reinterpret_cast<int32_t*>(base + L.sched_off);
   hipError_t e;
-  if (attn_impl() == 1) {
+  const int impl = attn_impl();
+  if (impl == 1) {
     e = fp::launch_attn(a, p->dtype, p->head_dim,
                         static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap, s);
+  } else if (impl == 3) {
+    e = fp::launch_attn_wide(a, p->dtype, p->head_dim,
+                             static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap, s);
   } else {
     int cus = 0;
     e = device_cus(&cus);

@@ -67,6 +67,8 @@ hipError_t launch_pool(const PoolArgs& a, int dtype, int head_dim, int64_t grid,
 hipError_t launch_search(const SearchArgs& a, int dtype, int head_dim, int64_t grid,
                          bool from_scores, hipStream_t s);
 hipError_t launch_attn(const AttnArgs& a, int dtype, int head_dim, int64_t grid, hipStream_t s);
+hipError_t launch_attn_wide(const AttnArgs& a, int dtype, int head_dim, int64_t grid,
+                            hipStream_t s);
 hipError_t launch_attn_pp(const AttnArgs& a, int dtype, int head_dim, int num_wg, hipStream_t s);
 
 }  // namespace fp

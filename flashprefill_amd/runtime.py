@@ -21,9 +21,10 @@ BLOCK = 128
 def attn_key_tile() -> int:
     """Keys per online-softmax step of the attention kernel the library runs:
     128 for the one-workgroup-per-row kernel (default), 64 for the persistent
-    kernel selected with FLASHPREFILL_ATTN=persistent."""
+    kernel (FLASHPREFILL_ATTN=persistent) and the 64-queries-per-wave kernel
+    (FLASHPREFILL_ATTN=wide)."""
     import os
-    return 64 if os.environ.get("FLASHPREFILL_ATTN") == "persistent" else 128
+    return 64 if os.environ.get("FLASHPREFILL_ATTN") in ("persistent", "wide") else 128
 
 
 def _dtype_code(t: torch.Tensor) -> int:

@@ -20,8 +20,9 @@ from tests._parity import OUT_MAX_ABS, OUT_MEAN_ABS, run_stages
 
 pytestmark = pytest.mark.gpu
 
-# both attention kernels: one workgroup per row (default) and the persistent one
-KERNELS = ["rows", "persistent"]
+# the attention kernels: one workgroup per row (default), the persistent one and
+# the 64-queries-per-wave one
+KERNELS = ["rows", "persistent", "wide"]
 
 
 @pytest.fixture(params=KERNELS)
