@@ -33,13 +33,15 @@ __device__ __forceinline__ float exp2_rn(float x) {
 }
 
 // Select over p (pl) and m (ml) of one row held in LDS; writes the ascending
-// index list and its length. Uses 256 threads.
+// index list and its length. Uses 256 threads; `scratch` is 64 bytes of LDS
+// for the block reductions (the query block's area once scoring is done, so
+// that the kernel's LDS stays at 40 KB and four workgroups fit on a CU).
 __device__ void select_row(float* pl, const float* ml, int n, int i, int nb,
-                           const SearchArgs& a, int32_t* list, int32_t* count) {
+                           const SearchArgs& a, int32_t* list, int32_t* count, void* scratch) {
 #pragma clang fp contract(off)
-  __shared__ float redf[4];
-  __shared__ double redd[4];
-  __shared__ int wtot[4];
+  float* redf = static_cast<float*>(scratch);
+  double* redd = reinterpret_cast<double*>(static_cast<char*>(scratch) + 16);
+  int* wtot = reinterpret_cast<int*>(static_cast<char*>(scratch) + 48);
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
 
   float lm = -INFINITY;
@@ -90,11 +92,14 @@ __device__ __forceinline__ int qswz(int r) {
   else return (r >> 1) & 7;
 }
 
+// dynamic LDS ahead of p / m: the query block, or the reductions' 64 bytes
 template <int D, bool FROM_SCORES>
-constexpr size_t search_q_bytes() { return FROM_SCORES ? 0 : kBlock * D * 2; }
+constexpr size_t search_q_bytes() { return FROM_SCORES ? 64 : kBlock * D * 2; }
 
 template <typename T, int D, bool FROM_SCORES>
-__global__ __launch_bounds__(256, 3) void k_search(SearchArgs a) {
+__global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
+  // 4 workgroups per CU: 4 x (32 KB query block + 2 x 4 KB p / m at 1024
+  // blocks) = 160 KB of LDS, and at most 128 VGPRs per wave
   extern __shared__ uint4 dyn4[];
   uint4* sq = dyn4;  // the query block (score mode only)
   float* pl = reinterpret_cast<float*>(reinterpret_cast<char*>(dyn4) + search_q_bytes<D, FROM_SCORES>());
@@ -206,7 +211,7 @@ __global__ __launch_bounds__(256, 3) void k_search(SearchArgs a) {
   __syncthreads();
   int32_t* list = a.idx + row_tri;
   int32_t* count = a.cnt + static_cast<int64_t>(h) * a.nb_sum_cap + tile_b + i;
-  select_row(pl, ml, n, i, nb, a, list, count);
+  select_row(pl, ml, n, i, nb, a, list, count, dyn4);
 }
 
 template <typename T, int D, bool FROM_SCORES>
