@@ -70,8 +70,6 @@ int validate(const fp_problem* p) {
     if (strides[s] >= (int64_t(1) << 24))
       return fail(FP_E_UNSUPPORTED, "strides of 2^24 elements or more are not supported");
   if (p->min_budget < 0) return fail(FP_E_INVALID_ARG, "min_budget < 0");
-  if (p->min_budget > 0)
-    return fail(FP_E_UNSUPPORTED, "min_budget > 0 is not implemented on the GPU path");
   if (p->native_normalize != 0 && p->native_normalize != 1)
     return fail(FP_E_INVALID_ARG, "native_normalize must be 0 or 1");
   return FP_OK;

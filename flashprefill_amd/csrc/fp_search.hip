@@ -32,16 +32,80 @@ __device__ __forceinline__ float exp2_rn(float x) {
   return static_cast<float>(exp2(static_cast<double>(x)));
 }
 
+// fp32 -> uint32 whose unsigned order is the float order (non-NaN values)
+__device__ __forceinline__ uint32_t sort_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// LDS scratch of select_row: block-reduction slots and the radix histogram
+constexpr int kSelectScratch = 64 + 32 + 256 * 4;
+
+// The min_budget largest scores of a row, ranked by (score desc, j asc) as
+// the oracle ranks them (native path, ops/flashprefill_native_forward.py:
+// 353-357, where torch.topk leaves the order of equal scores unspecified):
+// returns the key of the budget-th entry and, in `need_eq`, how many of the
+// entries with exactly that key are taken (lowest j first). Radix select over
+// the sortable 32-bit keys, 8 bits per pass, MSB first.
+__device__ uint32_t budget_threshold(const float* pl, int n, int kk, uint32_t* hist, int* pick,
+                                     int& need_eq) {
+  const int t = threadIdx.x, lane = t & 63;
+  uint32_t prefix = 0, pmask = 0;
+  int need = kk;
+  for (int shift = 24; shift >= 0; shift -= 8) {
+    hist[t] = 0;  // 256 bins, one per thread
+    __syncthreads();
+    for (int j = t; j < n; j += 256) {
+      const uint32_t key = sort_key(pl[j]);
+      if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255], 1u);
+    }
+    __syncthreads();
+    if (t < 64) {  // wave 0: the bin holding the need-th largest key
+      const int b0 = 255 - 4 * lane;  // this lane's bins b0 .. b0-3, descending
+      const int c0 = hist[b0], c1 = hist[b0 - 1], c2 = hist[b0 - 2], c3 = hist[b0 - 3];
+      const int sl = c0 + c1 + c2 + c3;
+      int incl = sl;
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o);
+        if (lane >= o) incl += y;
+      }
+      const uint64_t hit = __ballot(incl >= need);
+      if (lane == __ffsll(static_cast<long long>(hit)) - 1) {
+        int rem = need - (incl - sl), bin = b0;
+        if (rem > c0) {
+          rem -= c0, --bin;
+          if (rem > c1) {
+            rem -= c1, --bin;
+            if (rem > c2) rem -= c2, --bin;
+          }
+        }
+        pick[0] = bin;
+        pick[1] = rem;
+      }
+    }
+    __syncthreads();
+    prefix |= static_cast<uint32_t>(pick[0]) << shift;
+    pmask |= 255u << shift;
+    need = pick[1];
+    __syncthreads();  // pick and hist are rewritten by the next pass
+  }
+  need_eq = need;
+  return prefix;
+}
+
 // Select over p (pl) and m (ml) of one row held in LDS; writes the ascending
-// index list and its length. Uses 256 threads; `scratch` is 64 bytes of LDS
-// for the block reductions (the query block's area once scoring is done, so
-// that the kernel's LDS stays at 40 KB and four workgroups fit on a CU).
-__device__ void select_row(float* pl, const float* ml, int n, int i, int nb,
-                           const SearchArgs& a, int32_t* list, int32_t* count, void* scratch) {
+// index list and its length. Uses 256 threads; `scratch` is kSelectScratch
+// bytes of LDS (the query block's area once scoring is done, so that the
+// kernel's LDS stays at 40 KB and four workgroups fit on a CU). ml is
+// overwritten (with the min_budget flags).
+__device__ void select_row(float* pl, float* ml, int n, int i, int nb, const SearchArgs& a,
+                           int32_t* list, int32_t* count, void* scratch) {
 #pragma clang fp contract(off)
   float* redf = static_cast<float*>(scratch);
   double* redd = reinterpret_cast<double*>(static_cast<char*>(scratch) + 16);
   int* wtot = reinterpret_cast<int*>(static_cast<char*>(scratch) + 48);
+  int* pick = reinterpret_cast<int*>(static_cast<char*>(scratch) + 64);
+  uint32_t* hist = reinterpret_cast<uint32_t*>(static_cast<char*>(scratch) + 96);
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
 
   float lm = -INFINITY;
@@ -65,12 +129,34 @@ __device__ void select_row(float* pl, const float* ml, int n, int i, int nb,
   const float thr = maxS * a.alpha;
   const bool last_rows = i >= nb - a.last_n;
 
+  // min_budget: flag the budget largest scores in ml (1.0 = forced on)
+  const int kk = min(a.min_budget, n);
+  if (kk > 0) {
+    int need_eq;
+    const uint32_t kstar = budget_threshold(pl, n, kk, hist, pick, need_eq);
+    int eq_running = 0;
+    for (int base = 0; base < n; base += 256) {
+      const int j = base + t;
+      const uint32_t key = j < n ? sort_key(pl[j]) : 0u;
+      const bool eq = j < n && key == kstar;
+      const uint64_t bal = __ballot(eq);
+      if (lane == 0) wtot[w] = __popcll(bal);
+      __syncthreads();
+      int off = eq_running;
+      for (int k = 0; k < w; ++k) off += wtot[k];
+      if (j < n) ml[j] = (key > kstar || (eq && off + lanes_below(bal) < need_eq)) ? 1.0f : 0.0f;
+      eq_running += wtot[0] + wtot[1] + wtot[2] + wtot[3];
+      __syncthreads();
+    }
+  }
+
   int running = 0;
   for (int base = 0; base < n; base += 256) {
     const int j = base + t;
     bool keep = false;
     if (j < n) {
-      keep = (pl[j] >= thr) || (j < a.sink) || (i - j < a.window) || last_rows;
+      keep = (pl[j] >= thr) || (j < a.sink) || (i - j < a.window) || last_rows ||
+             (kk > 0 && ml[j] != 0.0f);
     }
     const uint64_t bal = __ballot(keep);
     if (lane == 0) wtot[w] = __popcll(bal);
@@ -92,9 +178,9 @@ __device__ __forceinline__ int qswz(int r) {
   else return (r >> 1) & 7;
 }
 
-// dynamic LDS ahead of p / m: the query block, or the reductions' 64 bytes
+// dynamic LDS ahead of p / m: the query block, or select_row's scratch
 template <int D, bool FROM_SCORES>
-constexpr size_t search_q_bytes() { return FROM_SCORES ? 64 : kBlock * D * 2; }
+constexpr size_t search_q_bytes() { return FROM_SCORES ? kSelectScratch : kBlock * D * 2; }
 
 template <typename T, int D, bool FROM_SCORES>
 __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {

@@ -46,7 +46,8 @@ def seq_slices(cu: Sequence[int]):
 
 
 def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n=2,
-               native=False, check_oracle_scores=True, attention=True) -> StageReport:
+               native=False, check_oracle_scores=True, attention=True,
+               min_budget=0) -> StageReport:
     """Run plan/pool/search(dump)/select/attn on the GPU and compare each stage
     with the oracle. q/k/v are CPU tensors (T, H, d); cu_list python ints."""
     dev = torch.device("cuda:0")
@@ -54,7 +55,8 @@ def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n
     od = torch.full_like(qd, float("nan"))
     cu = torch.tensor(cu_list, dtype=torch.int32, device=dev)
     call = FlashPrefillCall(qd, kd, vd, od, cu, max_seq_len, alpha=alpha, attention_sink=sink,
-                            window_size=window, last_n_block=last_n, native_normalize=native)
+                            window_size=window, last_n_block=last_n, native_normalize=native,
+                            min_budget=min_budget)
     rep = StageReport()
     call.plan()
     call.pool()
@@ -88,11 +90,11 @@ def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n
         # exact selection from the GPU's fp32 scores
         sel_g = O.select_from_scores(gp[b].nan_to_num(0.0).where(tril, torch.zeros(())),
                                      gm[b].where(tril, torch.tensor(float("-inf"))),
-                                     native, alpha, sink, window, last_n)
+                                     native, alpha, sink, window, last_n, min_budget)
         rep.sel_from_gpu_scores_mismatch += int((sel_g != gpu_sel[b]).sum())
         # end-to-end selection vs the oracle's own scores (tie flips)
         p_e, m_e = O.block_score(q[s0:s1], mk_o)
-        sel_e = O.select_from_scores(p_e, m_e, native, alpha, sink, window, last_n)
+        sel_e = O.select_from_scores(p_e, m_e, native, alpha, sink, window, last_n, min_budget)
         rep.e2e_flips += int((sel_e != gpu_sel[b]).sum())
         rep.cells += int(tril.sum())
         rep.density += int(gpu_sel[b].sum())
@@ -109,7 +111,7 @@ def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n
             if s1 == s0:
                 continue
             want = O.select_from_scores(oracle_ps[b], oracle_ms[b], native, alpha, sink, window,
-                                        last_n)
+                                        last_n, min_budget)
             rep.sel_from_oracle_scores_mismatch += int((sel2[b] != want).sum())
         # restore the GPU's own selection for the attention stage
         call.search()

@@ -78,7 +78,7 @@ def test_layout_bounds():
     ("max_seq_len", 0, _lib.FP_E_INVALID_ARG),
     ("q", 0x10002, _lib.FP_E_INVALID_ARG),
     ("k_stride_tok", 100, _lib.FP_E_INVALID_ARG),
-    ("min_budget", 4, _lib.FP_E_UNSUPPORTED),
+    ("min_budget", -1, _lib.FP_E_INVALID_ARG),
     ("native_normalize", 2, _lib.FP_E_INVALID_ARG),
 ])
 def test_invalid_arguments_rejected_on_host(field, value, code):

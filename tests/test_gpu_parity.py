@@ -78,6 +78,16 @@ def test_qwen_heads_not_multiple_of_8_fp16_d64(attn_kernel):
     _check(run_stages(q, k, v, cu, 1000, alpha=0.08))
 
 
+@pytest.mark.parametrize("min_budget", [3, 40])
+def test_native_min_budget(min_budget):
+    # the min_budget largest scores of a row are forced on (native path,
+    # ops/flashprefill_native_forward.py:353-357); 40 exceeds the causal
+    # width of the first rows, where every block is then selected
+    lens = [2048, 700]
+    q, k, v, cu = _rand_inputs(lens, 4, 1, 128, torch.bfloat16, 5, scale=2.0)
+    _check(run_stages(q, k, v, cu, 2048, alpha=0.9, native=True, min_budget=min_budget))
+
+
 def test_selection_params_sweep():
     lens = [1024, 700]
     q, k, v, cu = _rand_inputs(lens, 4, 1, 128, torch.bfloat16, 3, scale=2.0)
