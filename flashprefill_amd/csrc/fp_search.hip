@@ -98,13 +98,19 @@ __device__ uint32_t budget_threshold(const float* pl, int n, int kk, uint32_t* h
 // bytes of LDS (the query block's area once scoring is done, so that the
 // kernel's LDS stays at 40 KB and four workgroups fit on a CU). ml is
 // overwritten (with the min_budget flags).
+//
+// Two block reductions: M = max_j m_j, then max_j S_j together with the
+// native row sum. Since the native division by (sum + 1e-9) is correctly
+// rounded and monotone, the max of the normalised scores is the normalised
+// max. The compaction loops use alternating count slots, one barrier per
+// 256 entries.
 __device__ void select_row(float* pl, float* ml, int n, int i, int nb, const SearchArgs& a,
                            int32_t* list, int32_t* count, void* scratch) {
 #pragma clang fp contract(off)
   float* redf = static_cast<float*>(scratch);
   double* redd = reinterpret_cast<double*>(static_cast<char*>(scratch) + 16);
-  int* wtot = reinterpret_cast<int*>(static_cast<char*>(scratch) + 48);
-  int* pick = reinterpret_cast<int*>(static_cast<char*>(scratch) + 64);
+  int* wtot = reinterpret_cast<int*>(static_cast<char*>(scratch) + 48);  // [2][4]
+  int* pick = reinterpret_cast<int*>(static_cast<char*>(scratch) + 80);
   uint32_t* hist = reinterpret_cast<uint32_t*>(static_cast<char*>(scratch) + 96);
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
 
@@ -113,19 +119,27 @@ __device__ void select_row(float* pl, float* ml, int n, int i, int nb, const Sea
   const float M = block_max(lm, redf);
 
   double ls = 0.0;
+  float lmax = 0.0f;
   for (int j = t; j < n; j += 256) {
-    const float s = pl[j] * exp2_rn(ml[j] - M);
-    pl[j] = s;
-    ls += static_cast<double>(s);
+    const float sj = pl[j] * exp2_rn(ml[j] - M);
+    pl[j] = sj;
+    ls += static_cast<double>(sj);
+    lmax = fmaxf(lmax, sj);
   }
+  lmax = wave_max(lmax);
+  if (a.native) ls = wave_sum_d(ls);
+  if (lane == 0) {
+    redf[w] = lmax;
+    redd[w] = ls;
+  }
+  __syncthreads();  // redf / redd are not written again in this row
+  float maxS = fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
   if (a.native) {
-    const float tot = static_cast<float>(block_sum_d(ls, redd));
+    const float tot = static_cast<float>(redd[0] + redd[1] + redd[2] + redd[3]);
     const float denom = tot + 1e-9f;
+    maxS = maxS / denom;
     for (int j = t; j < n; j += 256) pl[j] = pl[j] / denom;
   }
-  float lmax = 0.0f;
-  for (int j = t; j < n; j += 256) lmax = fmaxf(lmax, pl[j]);
-  const float maxS = block_max(lmax, redf);
   const float thr = maxS * a.alpha;
   const bool last_rows = i >= nb - a.last_n;
 
@@ -135,23 +149,23 @@ __device__ void select_row(float* pl, float* ml, int n, int i, int nb, const Sea
     int need_eq;
     const uint32_t kstar = budget_threshold(pl, n, kk, hist, pick, need_eq);
     int eq_running = 0;
-    for (int base = 0; base < n; base += 256) {
+    for (int base = 0, c2 = 0; base < n; base += 256, c2 ^= 4) {
       const int j = base + t;
       const uint32_t key = j < n ? sort_key(pl[j]) : 0u;
       const bool eq = j < n && key == kstar;
       const uint64_t bal = __ballot(eq);
-      if (lane == 0) wtot[w] = __popcll(bal);
+      if (lane == 0) wtot[c2 + w] = __popcll(bal);
       __syncthreads();
       int off = eq_running;
-      for (int k = 0; k < w; ++k) off += wtot[k];
+      for (int k = 0; k < w; ++k) off += wtot[c2 + k];
       if (j < n) ml[j] = (key > kstar || (eq && off + lanes_below(bal) < need_eq)) ? 1.0f : 0.0f;
-      eq_running += wtot[0] + wtot[1] + wtot[2] + wtot[3];
-      __syncthreads();
+      eq_running += wtot[c2] + wtot[c2 + 1] + wtot[c2 + 2] + wtot[c2 + 3];
     }
+    __syncthreads();  // the count slots are reused below
   }
 
   int running = 0;
-  for (int base = 0; base < n; base += 256) {
+  for (int base = 0, c2 = 0; base < n; base += 256, c2 ^= 4) {
     const int j = base + t;
     bool keep = false;
     if (j < n) {
@@ -159,13 +173,13 @@ __device__ void select_row(float* pl, float* ml, int n, int i, int nb, const Sea
              (kk > 0 && ml[j] != 0.0f);
     }
     const uint64_t bal = __ballot(keep);
-    if (lane == 0) wtot[w] = __popcll(bal);
+    // slot set c2 was last read before the previous chunk's barrier
+    if (lane == 0) wtot[c2 + w] = __popcll(bal);
     __syncthreads();
     int off = running;
-    for (int k = 0; k < w; ++k) off += wtot[k];
+    for (int k = 0; k < w; ++k) off += wtot[c2 + k];
     if (keep) list[off + lanes_below(bal)] = j;
-    running += wtot[0] + wtot[1] + wtot[2] + wtot[3];
-    __syncthreads();
+    running += wtot[c2] + wtot[c2 + 1] + wtot[c2 + 2] + wtot[c2 + 3];
   }
   if (t == 0) *count = running;
 }
