@@ -80,6 +80,25 @@ def test_all_blocks_selected_is_dense_causal():
     _close(o, ref.permute(1, 0, 2))
 
 
+@pytest.mark.parametrize("kernel", ["rows", "persistent", "wide"])
+def test_all_blocks_selected_long_rows(kernel, monkeypatch):
+    # 8300 tokens: 65 blocks per row (the wide kernel reloads its 64-entry
+    # block-list chunk), a partial last block of 108 rows (its second half tile
+    # holds 44), dense causal attention against fp32 SDPA
+    monkeypatch.setenv("FLASHPREFILL_ATTN", kernel)
+    T, Hq, Hkv, d = 8300, 4, 1, 128
+    q, k, v = _rand((T, Hq, d), 21, scale=1.5), _rand((T, Hkv, d), 22, scale=1.5), _rand((T, Hkv, d), 23)
+    o = torch.empty(T, Hq, d, dtype=torch.bfloat16, device=DEV)
+    cu = torch.tensor([0, T], dtype=torch.int32, device=DEV)
+    flash_prefill_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), o, cu, T, 0.0)
+    torch.cuda.synchronize()
+    qq = q.float().permute(1, 0, 2).contiguous().to(DEV)
+    kk = k.float().permute(1, 0, 2).repeat_interleave(Hq // Hkv, 0).contiguous().to(DEV)
+    vv = v.float().permute(1, 0, 2).repeat_interleave(Hq // Hkv, 0).contiguous().to(DEV)
+    ref = torch.nn.functional.scaled_dot_product_attention(qq, kk, vv, is_causal=True)
+    _close(o, ref.permute(1, 0, 2).cpu())
+
+
 def test_status_flags_and_untouched_output():
     T, Hq, Hkv, d = 1000, 4, 1, 128
     q, k, v = _rand((T, Hq, d), 11).to(DEV), _rand((T, Hkv, d), 12).to(DEV), _rand((T, Hkv, d), 13).to(DEV)
