@@ -98,16 +98,13 @@ __device__ __forceinline__ void dma16_vaddr(void* lds_slice, const void* src) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, off"
                :: "s"(lds_addr(lds_slice)), "v"(src) : "memory", "m0");
 }
-// the same two loads with the LDS slice given as a wave-uniform LDS byte address
-__device__ __forceinline__ void dma16_saddr_at(uint32_t lds, const void* base, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, %2"
-               :: "s"(lds), "v"(voff), "s"(scalar_addr(base)) : "memory", "m0");
-}
-// one load: an address already held in SGPRs + 32-bit lane offset
-__device__ __forceinline__ void dma16_sbase_at(uint32_t lds, uint64_t sbase, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, %2"
+// one load whose scalar base and LDS address were formed by SALU (no VALU
+// write of an SGPR to wait for): only the M0 write needs a wait state
+__device__ __forceinline__ void dma16_sbase_m0(uint32_t lds, uint64_t sbase, uint32_t voff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 1\n\tglobal_load_lds_dwordx4 %1, %2"
                :: "s"(lds), "v"(voff), "s"(sbase) : "memory", "m0");
 }
+// one load: per-lane 64-bit address, LDS slice as a wave-uniform LDS byte address
 __device__ __forceinline__ void dma16_vaddr_at(uint32_t lds, const void* src) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, off"
                :: "s"(lds), "v"(src) : "memory", "m0");
@@ -143,13 +140,18 @@ __device__ __forceinline__ void issue_tile(uint4* lds, const uint16_t* base, int
                                            int lane) {
   constexpr int CH = TileLanes<D>::CH, RPW = TileLanes<D>::RPW, NI = TileLanes<D>::NI;
   if ((j + 1) * kBlock <= L) {
+    // one scalar base and LDS address per tile; the slices' offsets are
+    // scalar adds, so each load costs an add, the M0 write and one wait state
+    uint64_t sb = scalar_addr(reinterpret_cast<const char*>(base) +
+                              static_cast<int64_t>(j * kBlock + w * NI * RPW) * stride * 2);
+    const uint32_t l0 = lds_addr(lds + w * NI * 64);
+    // the base was written by VALU (readfirstlane): five wait states before
+    // a VMEM instruction reads it; every later use goes through this asm
+    asm volatile("s_nop 4" : "+s"(sb));
+    const uint64_t step = static_cast<uint64_t>(RPW) * static_cast<uint64_t>(stride) * 2;
 #pragma unroll
-    for (int q = 0; q < NI; ++q) {
-      const int slot = w * NI + q;
-      const char* sbase = reinterpret_cast<const char*>(base) +
-                          static_cast<int64_t>(j * kBlock + slot * RPW) * stride * 2;
-      dma16_saddr(lds + slot * 64, sbase, tl.off[q % TileLanes<D>::PER]);
-    }
+    for (int q = 0; q < NI; ++q)
+      dma16_sbase_m0(l0 + q * 1024, sb + q * step, tl.off[q % TileLanes<D>::PER]);
   } else {  // partial last block: rows past the end read row L-1 (masked keys, p = 0)
 #pragma unroll
     for (int q = 0; q < NI; ++q) {
@@ -184,30 +186,6 @@ struct HalfLanes {
   }
 };
 
-template <int D>
-__device__ __forceinline__ void issue_half(uint4* lds, const uint16_t* base, int64_t stride,
-                                           const HalfLanes<D>& tl, int j, int hf, int L, int w,
-                                           int lane) {
-  constexpr int CH = HalfLanes<D>::CH, RPW = HalfLanes<D>::RPW, NI = HalfLanes<D>::NI;
-  const int row0 = j * kBlock + 64 * hf;
-  if (row0 + 64 <= L) {
-    const char* sbase = reinterpret_cast<const char*>(base) + static_cast<int64_t>(row0) * stride * 2;
-#pragma unroll
-    for (int q = 0; q < NI; ++q) {
-      const int slot = w * NI + q;
-      dma16_saddr(lds + slot * 64, sbase, tl.off[q]);
-    }
-  } else {  // rows past the sequence end read row L-1 (masked keys, p = 0)
-#pragma unroll
-    for (int q = 0; q < NI; ++q) {
-      const int slot = w * NI + q;
-      const int r = slot * RPW + lane / CH;
-      const int c = (lane % CH) ^ swz<D>(r);
-      const int gk = min(row0 + r, L - 1);
-      dma16_vaddr(lds + slot * 64, base + static_cast<int64_t>(gk) * stride + 8 * c);
-    }
-  }
-}
 
 // Reductions over the two 32-lane halves of a wave (lane l with l ^ 32):
 // v_permlane32_swap exchanges the halves of its two operands, so max / sum

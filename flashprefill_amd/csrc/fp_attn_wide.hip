@@ -77,11 +77,14 @@ __device__ __forceinline__ void wide_tile(uint32_t lds, const uint16_t* base, in
   constexpr int CH = WideLanes<D>::CH, RPW = WideLanes<D>::RPW, NI = WideLanes<D>::NI;
   if (nvalid >= 64) {
     // one scalar base per tile; the slices' row offsets are scalar adds
-    const uint64_t sb = scalar_addr(base);
+    uint64_t sb = scalar_addr(base);
+    // the base was written by VALU (readfirstlane): five wait states before
+    // a VMEM instruction reads it; every later use goes through this asm
+    asm volatile("s_nop 4" : "+s"(sb));
 #pragma unroll
     for (int q = 0; q < NI; ++q) {
       const int slot = w * NI + q;
-      dma16_sbase_at(lds + slot * 1024, sb + static_cast<uint64_t>(slot * RPW * stride) * 2,
+      dma16_sbase_m0(lds + slot * 1024, sb + static_cast<uint64_t>(slot * RPW * stride) * 2,
                      tl.off[q % WideLanes<D>::PER]);
     }
   } else {

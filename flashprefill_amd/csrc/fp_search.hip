@@ -24,7 +24,7 @@
 // always yields the same index set: exp2 is evaluated in fp64 and rounded
 // once to fp32 (correctly rounded fp32 exp2), and the native row sum is
 // accumulated in fp64 and rounded once.
-#include "fp_internal.h"
+#include "fp_attn_common.h"
 
 namespace fp {
 
@@ -230,18 +230,21 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
     const int half = lane >> 5, l32 = lane & 31;
     const float c = a.sm_scale_log2;
     constexpr int CH = D / 8;
-    // stage the query block in LDS (rows past the sequence end are zero and
-    // still count for j < i); every wave reads it as MFMA A operands
-    // (rows 32*rg + l32, dims 16*s + 8*half .. +7)
-    for (int cidx = t; cidx < kBlock * CH; cidx += 256) {
-      const int r = cidx / CH, ch = cidx % CH;
-      uint4 val = zero4();
-      if (i * kBlock + r < L)
-        val = ld16(a.q + (t0 + static_cast<int64_t>(i) * kBlock + r) * a.qst +
-                   static_cast<int64_t>(h) * a.qhs + 8 * ch);
-      sq[r * CH + (ch ^ qswz<D>(r))] = val;
+    // stage the query block in LDS with direct-to-LDS loads (rows past the
+    // sequence end are then zeroed: they still count for j < i); every wave
+    // reads it as MFMA A operands (rows 32*rg + l32, dims 16*s + 8*half .. +7)
+    {
+      TileLanes<D> tq;
+      tq.init(a.qst, __builtin_amdgcn_readfirstlane(w), lane);
+      issue_tile<D>(sq, a.q + t0 * a.qst + static_cast<int64_t>(h) * a.qhs, a.qst, tq, i, L,
+                    __builtin_amdgcn_readfirstlane(w), lane);
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      if ((i + 1) * kBlock > L) {
+        for (int cidx = t; cidx < kBlock * CH; cidx += 256)
+          if (i * kBlock + cidx / CH >= L) sq[cidx] = zero4();
+        __syncthreads();
+      }
     }
-    __syncthreads();
     const int64_t mk_row = static_cast<int64_t>(a.Hkv) * D;
     const uint16_t* mkb = a.mk + tile_b * mk_row + static_cast<int64_t>(kvh) * D + 8 * half;
     const int ntiles = (n + 31) >> 5;
