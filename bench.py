@@ -1,10 +1,10 @@
-"""Benchmark of the FlashPrefill gfx950 path on BASELINE config 3.
+"""Benchmark of the FlashPrefill gfx950 path on the headline workload (config 3).
 
 One step = one full ``flash_prefill_varlen_func`` call (plan -> pool K ->
 search -> block-sparse attention) over a 131072-token single sequence with
 Llama-3-8B head shapes (32 q / 8 kv heads, d = 128, bf16, causal, block 128),
-inputs resident in HBM. Prints ONE JSON line (rank 0). See DESIGN.md for the
-definitions of every figure.
+inputs resident in HBM. Prints ONE JSON line (rank 0); each field is defined
+where main() fills it in.
 
     python bench.py [--gpus 1] [--steps 10] [--warmup 3]
 """
@@ -34,7 +34,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3,
-                    help="3 (default): the bench line; 2, 4 or 5: a report line for BASELINE "
+                    help="3 (default): the bench line; 2, 4 or 5: a report line for "
                          "config 2 (Llama shapes at 4K/16K/32K), 4 (Qwen2.5 varlen ragged) or "
                          "5 (64K decoder-layer attention block)")
     ap.add_argument("--seq-len", type=int, default=131072)
@@ -287,7 +287,7 @@ def _rounded(x):
 
 
 def other_config(args):
-    """BASELINE configs 2 (Llama shapes at 4K / 16K / 32K) and 4 (Qwen2.5 varlen
+    """Configs 2 (Llama shapes at 4K / 16K / 32K) and 4 (Qwen2.5 varlen
     ragged batch): one JSON report line, secondary to the config-3 bench line."""
     import torch
     from flashprefill_amd import synth
@@ -315,15 +315,15 @@ def other_config(args):
         results.append(_rounded(r))
         del q, k, v, cu
         torch.cuda.empty_cache()
-    print(json.dumps({"report": f"BASELINE config {args.config}", "n_gpus": 1, "dtype": "bf16",
+    print(json.dumps({"report": f"config {args.config}", "n_gpus": 1, "dtype": "bf16",
                       "data": "synthetic (flashprefill_amd/synth.py)",
                       "attention_kernel": attn_kernel_name(), "results": results}), flush=True)
 
 
 def decoder_layer_report(args):
-    """one prefill attention block at 64K tokens (hidden
+    """Config 5: one prefill attention block at 64K tokens (hidden
     4096, 32 q / 4 kv heads, d = 128, bf16, RoPE theta 1e6, random-init
-    weights, no q/k norm as in the BASELINE text): QKV projection -> RoPE ->
+    weights, no q/k norm, as the config describes it): QKV projection -> RoPE ->
     FlashPrefill (varlen signature, cu_seqlens = [0, S]) -> O projection."""
     import torch
     from flashprefill_amd import flash_prefill_varlen_func
@@ -349,7 +349,7 @@ def decoder_layer_report(args):
     nb = S // 128
     n_exec = int(call.counts()[:, :nb].sum().item())
     density = n_exec / (Hq * nb * (nb + 1) // 2)
-    rep = {"report": "BASELINE config 5", "n_gpus": 1, "dtype": "bf16",
+    rep = {"report": "config 5", "n_gpus": 1, "dtype": "bf16",
            "data": "synthetic: hidden states ~ N(0,1), random-init weights (seed 5)",
            "attention_kernel": attn_kernel_name(),
            "config": {"seq_len": S, "hidden": hidden, "num_q_heads": Hq, "num_kv_heads": Hkv,
@@ -431,7 +431,7 @@ def main():
         "data": ("synthetic: seeded structured Q/K/V ~ N(0,1)/sqrt(d) with sinks, 64 stripe "
                  "runs, rotary local band, topic segments, 8 hot blocks/head "
                  "(flashprefill_amd/synth.py)"),
-        "config": {"workload": "BASELINE config 3: 131072-token single-sequence prefill attention, "
+        "config": {"workload": "config 3: 131072-token single-sequence prefill attention, "
                                "Llama-3-8B heads", "seq_len": S, "num_q_heads": Hq,
                    "num_kv_heads": Hkv, "head_dim": d, "block_size": 128, "alpha": args.alpha,
                    "attention_sink": 2, "window_size": 4, "last_n_block": 2, "seed": args.seed},

@@ -70,7 +70,7 @@ class SynthSpec:
 
 
 def config1_spec(seed: int = 0) -> SynthSpec:
-    """4096 tokens, 8q/2kv, d=64, fp32, unscaled N(0,1),
+    """Config 1: 4096 tokens, 8q/2kv, d=64, fp32, unscaled N(0,1),
     K rows 0-3 x4 (sink) and 16 stripe columns."""
     return SynthSpec(seq_lens=(4096,), num_q_heads=8, num_kv_heads=2, head_dim=64,
                      dtype=torch.float32, seed=seed, scaled=False, sink_logit=0.0,
@@ -79,14 +79,14 @@ def config1_spec(seed: int = 0) -> SynthSpec:
 
 
 def llama_spec(seq_len: int, seed: int, dtype=torch.bfloat16) -> SynthSpec:
-    """BASELINE configs 2/3: Llama-3-8B head shapes (32q/8kv, d=128)."""
+    """Configs 2/3: Llama-3-8B head shapes (32q/8kv, d=128)."""
     return SynthSpec(seq_lens=(seq_len,), num_q_heads=32, num_kv_heads=8, head_dim=128,
                      dtype=dtype, seed=seed)
 
 
 def qwen_varlen_spec(seq_lens: Sequence[int] = (262144, 65536, 17408, 3072, 1024),
                      seed: int = 7, dtype=torch.bfloat16) -> SynthSpec:
-    """Qwen2.5-7B head shapes (28q/4kv, d=128), ragged batch."""
+    """Config 4: Qwen2.5-7B head shapes (28q/4kv, d=128), ragged batch."""
     return SynthSpec(seq_lens=tuple(int(s) for s in seq_lens), num_q_heads=28,
                      num_kv_heads=4, head_dim=128, dtype=dtype, seed=seed)
 

@@ -1,4 +1,4 @@
-"""Parity at the full BASELINE config-3 size (131072 tokens, 32 q / 8 kv heads,
+"""Parity at the full config-3 size (131072 tokens, 32 q / 8 kv heads,
 d = 128, bf16): the whole operator runs on the GPU through the C ABI, and a
 sample of (head, q-block) rows from light to heavy is recomputed by the
 oracle's row pipeline (pooled K of all blocks, scores, normalisation,
