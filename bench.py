@@ -79,9 +79,14 @@ def traffic_file(S):
     return os.path.join(ROOT, "profiles", f"attn_traffic_llama{S // 1024}k_{attn_kernel_name()}.json")
 
 
+def stage_traffic_file(S):
+    return os.path.join(ROOT, "profiles", f"search_pool_traffic_llama{S // 1024}k.json")
+
+
 def traffic_probe(args):
-    """One attention launch on the bench input and one plain 1 GiB copy, for
-    the counter passes of --collect-traffic."""
+    """One call of each stage (plan, pool, search, attention) on the bench
+    input and one plain 1 GiB copy, for the counter passes of
+    --collect-traffic."""
     import torch
     from flashprefill_amd import synth
     from flashprefill_amd.runtime import FlashPrefillCall
@@ -102,8 +107,8 @@ def traffic_probe(args):
 def collect_traffic(args):
     """Two rocprofv3 counter passes over --traffic-probe (started as child
     processes; this process never touches the GPU). FETCH_SIZE / WRITE_SIZE
-    of the attention dispatch are scaled by (known bytes / counter reading)
-    of the copy kernel in the same pass."""
+    of the attention, pooling and search dispatches are scaled by (known
+    bytes / counter reading) of the copy kernel in the same pass."""
     import csv
     import glob
     import subprocess
@@ -123,6 +128,8 @@ def collect_traffic(args):
                 for row in csv.DictReader(open(f)):
                     name = row["Kernel_Name"]
                     key = ("attn" if f"fp::{attn_kernel_name()}<" in name else
+                           "pool" if "fp::k_pool<" in name else
+                           "search" if "fp::k_search<" in name else
                            "copy" if "copy" in name.lower() else None)
                     if key is None or row["Counter_Name"] != ctr:
                         continue
@@ -136,6 +143,10 @@ def collect_traffic(args):
             scale = COPY_BYTES / (copy_kib * 1024.0)
             res[ctr] = {"attn_kib": attn_kib, "copy_kib": copy_kib, "copy_scale": scale,
                         "attn_bytes": attn_kib * 1024.0 * scale}
+            for st in ("pool", "search"):
+                if st in vals:
+                    res[ctr][st + "_kib"] = vals[st][-1]
+                    res[ctr][st + "_bytes"] = vals[st][-1] * 1024.0 * scale
     out = {
         "kernel": attn_kernel_name(), "workload": f"bench.py config 3, seq_len {args.seq_len}, "
         f"seed {args.seed}, alpha {args.alpha}",
@@ -150,6 +161,17 @@ def collect_traffic(args):
     with open(traffic_file(args.seq_len), "w") as fh:
         json.dump(out, fh, indent=1)
     print(json.dumps(out), flush=True)
+    stages = {"workload": out["workload"], "command": out["command"],
+              "calibration": out["calibration"]}
+    for st, kern in (("pool", "k_pool"), ("search", "k_search")):
+        if f"{st}_bytes" in res["FETCH_SIZE"] and f"{st}_bytes" in res["WRITE_SIZE"]:
+            stages[kern] = {"fetch_bytes": res["FETCH_SIZE"][f"{st}_bytes"],
+                            "write_bytes": res["WRITE_SIZE"][f"{st}_bytes"],
+                            "traffic_bytes": res["FETCH_SIZE"][f"{st}_bytes"] +
+                            res["WRITE_SIZE"][f"{st}_bytes"]}
+    with open(stage_traffic_file(args.seq_len), "w") as fh:
+        json.dump(stages, fh, indent=1)
+    print(json.dumps(stages), flush=True)
 
 
 def dense_causal_flops(S, Hq, d):
@@ -219,6 +241,8 @@ def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines):
         call.search()
 
     ms_search = timed(search_stage, max(3, steps))
+    ms_pool = timed(call.pool, max(3, steps))
+    ms_score = timed(call.search, max(3, steps))
     ms_attn = timed(call.attn, max(3, steps))
     assert call.status() == 0
     tile, _, _, _ = call.seq_tables()
@@ -228,6 +252,7 @@ def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines):
     dense_flops = sum(dense_causal_flops(s, Hq, d) for s in seq_lens)
     out = {
         "ms_total": ms_total, "ms_search": ms_search, "ms_attn": ms_attn,
+        "ms_pool": ms_pool, "ms_score": ms_score,
         "search_share": ms_search / ms_total, "executed_blocks": n_exec,
         "density": n_exec / causal_blocks, "executed_tflops": exec_tflops,
         "mfma_frac": exec_tflops / PEAK_BF16_TFLOPS,
@@ -407,6 +432,35 @@ def main():
         print("bench: CPU baseline (oracle sample)", file=sys.stderr, flush=True)
         cpu = cpu_baseline(q, k, v, args.alpha, args.cpu_seconds)
 
+    # HBM roofline of the pooling and search kernels: algorithmic bytes per
+    # launch (pool: read K, write pooled K; search: read Q and pooled K, write
+    # the index lists and counts) and the measured HBM traffic, over each
+    # kernel's own time
+    elt = q.element_size()
+    nb = (S + 127) // 128
+    algo = {"k_pool": k.numel() * elt + nb * Hkv * d * elt,
+            "k_search": q.numel() * elt + nb * Hkv * d * elt + 4 * (n_exec + Hq * nb)}
+    stage_ms = {"k_pool": r["ms_pool"], "k_search": r["ms_score"]}
+    stage_traffic = {}
+    stf = stage_traffic_file(S)
+    if os.path.exists(stf):
+        with open(stf) as fh:
+            sj = json.load(fh)
+        if str(S) in sj.get("workload", ""):
+            stage_traffic = {kk: sj[kk]["traffic_bytes"] for kk in ("k_pool", "k_search")
+                             if kk in sj}
+    search_roofline = {"bound": "hbm", "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                       "traffic_source": os.path.relpath(stf, ROOT) if stage_traffic else None,
+                       "kernels": {}}
+    for kk in ("k_pool", "k_search"):
+        ach = algo[kk] / (stage_ms[kk] * 1e-3) / 1e9
+        ent = {"ms": round(stage_ms[kk], 4), "algorithmic_bytes": int(algo[kk]),
+               "achieved": round(ach, 1), "frac": round(ach / PEAK_HBM_GBPS, 4)}
+        if kk in stage_traffic:
+            ent["traffic"] = int(stage_traffic[kk])
+            ent["traffic_GBps"] = round(stage_traffic[kk] / (stage_ms[kk] * 1e-3) / 1e9, 1)
+        search_roofline["kernels"][kk] = ent
+
     traffic, traffic_src = None, None
     tf = traffic_file(S)
     if os.path.exists(tf):
@@ -449,6 +503,7 @@ def main():
                      "traffic": traffic, "traffic_unit": "bytes per launch (HBM, calibrated "
                      "FETCH_SIZE + WRITE_SIZE)", "traffic_source": traffic_src,
                      "algorithmic_kv_bytes": n_exec * 2 * 128 * d * q.element_size()},
+        "search_roofline": search_roofline,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
