@@ -1,0 +1,83 @@
+"""Seeded random configurations through every stage, against the oracle.
+
+Each case draws sequence lengths (including 1-token and partial-block
+sequences), head counts with a GQA ratio, head dim, dtype, selection
+parameters and the native / varlen mode, and runs the staged parity check:
+pooled K, block scores, exact selection in both directions from identical
+fp32 scores, and the attention output within the bf16 tolerance. The three
+attention kernels take turns. The sequences are short (at most ~10 blocks),
+so sink / window / last-n rules keep most blocks: these cases stress the
+edges (1-token and partial blocks, GQA ratios, d = 64, fp16, native mode,
+min_budget); sparse selection at length is covered by the structured 4K and
+128K tests."""
+
+import random
+
+import pytest
+import torch
+
+from tests._parity import OUT_MAX_ABS, OUT_MEAN_ABS, run_stages
+
+pytestmark = pytest.mark.gpu
+KERNELS = ["rows", "persistent", "wide"]
+
+
+def _case(seed):
+    rnd = random.Random(seed)
+    nseq = rnd.randint(1, 4)
+    lens = [rnd.choice([1, rnd.randint(2, 127), rnd.randint(128, 1500), 128 * rnd.randint(1, 10)])
+            for _ in range(nseq)]
+    hkv = rnd.choice([1, 2, 4])
+    hq = hkv * rnd.choice([1, 2, 4, 7])
+    d = rnd.choice([64, 128])
+    dtype = rnd.choice([torch.bfloat16, torch.float16])
+    params = dict(alpha=rnd.choice([0.0, 0.05, 0.12, 0.18, 0.5, 0.9]),
+                  sink=rnd.randint(0, 4), window=rnd.randint(0, 6), last_n=rnd.randint(0, 3),
+                  native=rnd.random() < 0.3)
+    if params["native"] and rnd.random() < 0.5:
+        params["min_budget"] = rnd.randint(1, 12)
+    # score spread: unit-scale inputs give flat block scores (every block
+    # kept); larger Q/K scales, sink rows and a shared direction in a few key
+    # blocks give peaked, sparse selections
+    shape = dict(scale=rnd.uniform(1.0, 4.0), sink=rnd.random() < 0.7, stripes=rnd.randint(0, 4))
+    return lens, hq, hkv, d, dtype, params, shape
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_configuration(seed, monkeypatch):
+    lens, hq, hkv, d, dtype, params, shape = _case(1000 + seed)
+    kernel = KERNELS[seed % len(KERNELS)]
+    monkeypatch.setenv("FLASHPREFILL_ATTN", kernel)
+    g = torch.Generator().manual_seed(seed)
+    T = sum(lens)
+    q = torch.randn(T, hq, d, generator=g) * shape["scale"]
+    k = torch.randn(T, hkv, d, generator=g) * shape["scale"]
+    v = torch.randn(T, hkv, d, generator=g)
+    cu = [0]
+    for s in lens:
+        cu.append(cu[-1] + s)
+    u = torch.randn(d, generator=g)
+    u = u / u.norm()
+    for b in range(len(lens)):
+        a0, a1 = cu[b], cu[b + 1]
+        if shape["sink"]:
+            k[a0:min(a0 + 4, a1)] *= 4.0
+        for _ in range(shape["stripes"]):  # a key block aligned with the queries' shared direction
+            if a1 - a0 >= 128:
+                j0 = a0 + 128 * int(torch.randint(0, (a1 - a0) // 128, (1,), generator=g))
+                k[j0:j0 + 128] += 3.0 * shape["scale"] * u
+    q += 0.5 * shape["scale"] * u
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    print(f"\n  seed={seed} kernel={kernel} lens={lens} hq={hq} hkv={hkv} d={d} {dtype} {params} "
+          f"{shape}", flush=True)
+    rep = run_stages(q, k, v, cu, max(lens), **params)
+    print(f"  flips={rep.e2e_flips}/{rep.cells} density={rep.density:.3f} "
+          f"out_max={rep.out_max_abs:.2e} out_mean={rep.out_mean_abs:.2e}", flush=True)
+    assert rep.pool_ulp <= 1
+    assert rep.m_max_rel < 1e-4
+    assert rep.p_max_rel < 1e-3
+    assert rep.sel_from_gpu_scores_mismatch == 0
+    assert rep.sel_from_oracle_scores_mismatch == 0
+    assert rep.e2e_flips <= max(2, 2e-3 * rep.cells)
+    assert rep.out_max_abs <= OUT_MAX_ABS
+    assert rep.out_mean_abs <= OUT_MEAN_ABS
