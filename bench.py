@@ -71,12 +71,13 @@ COPY_BYTES = 1 << 30  # calibration copy: 1 GiB read + 1 GiB written
 
 
 def attn_kernel_name():
-    return {"persistent": "k_attn_pp", "wide": "k_attn_wide"}.get(
+    return {"persistent": "k_attn_pp", "wide": "k_attn_wide", "pipe": "k_attn_wide"}.get(
         os.environ.get("FLASHPREFILL_ATTN", ""), "k_attn")
 
 
 def traffic_file(S):
-    return os.path.join(ROOT, "profiles", f"attn_traffic_llama{S // 1024}k_{attn_kernel_name()}.json")
+    tag = "k_attn_pipe" if os.environ.get("FLASHPREFILL_ATTN") == "pipe" else attn_kernel_name()
+    return os.path.join(ROOT, "profiles", f"attn_traffic_llama{S // 1024}k_{tag}.json")
 
 
 def stage_traffic_file(S):

@@ -30,9 +30,11 @@
 //
 // Numerics follow the reference loop: m starts at -inf and l at 1.0, one
 // 128-key tile per selected block, alpha = exp2(m_old - m_new) with NaN -> 1,
-// l accumulates the fp32 p, P is rounded to the input dtype before P.V, the
-// diagonal block masks key > query, and O = acc * (1/l). The accumulator is
-// rescaled only when some row's max moved (alpha == 1 makes it a no-op).
+// P is rounded to the input dtype before P.V, the diagonal block masks
+// key > query, and O = acc * (1/l). Two deliberate differences, both at
+// rounding level: m is the max of conditional rescaling (it moves only when a
+// block's max exceeds it by more than kRescaleSlack, so P <= 2^8), and l adds
+// the rounded P (v_dot2c, two scores per instruction) instead of the fp32 p.
 #include "fp_attn_common.h"
 
 namespace fp {
@@ -89,26 +91,34 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
 #pragma unroll
     for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[t4][v]);
   mx = fmaxf(mx, xor32_f(mx));
-  const float m_new = fmaxf(st.m_run, mx * c);
-  float alpha = __builtin_amdgcn_exp2f(st.m_run - m_new);
-  if (alpha != alpha) alpha = 1.0f;
-  float psum = 0.0f;
-#pragma unroll
-  for (int t4 = 0; t4 < 4; ++t4)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const float p = __builtin_amdgcn_exp2f(fmaf(s[t4][v], c, -m_new));
-      s[t4][v] = p;
-      psum += p;
-    }
-  st.l_part = st.l_part * alpha + psum;
-  st.m_run = m_new;
-  if (__ballot(alpha != 1.0f)) {
+  const float m_tile = mx * c;
+  // the running max moves (and O, l are rescaled) only when some row of the
+  // wave exceeds it by more than kRescaleSlack; always on the row's first block
+  if (__ballot(m_tile > st.m_run + kRescaleSlack)) {
+    const float m_new = fmaxf(st.m_run, m_tile);
+    float alpha = __builtin_amdgcn_exp2f(st.m_run - m_new);
+    if (alpha != alpha) alpha = 1.0f;
+    st.l_part *= alpha;
+    st.m_run = m_new;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int v = 0; v < 16; ++v) st.o[dt][v] *= alpha;
   }
+  // P rounded to the input type, packed as the B operands of P.V; l adds the
+  // rounded P that P.V consumes
+  uint32_t pk[4][8];
+  float psum[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int t4 = 0; t4 < 4; ++t4)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(s[t4][2 * e], c, -st.m_run));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(s[t4][2 * e + 1], c, -st.m_run));
+      pk[t4][e] = pack2<T>(p0, p1);
+      psum[e & 1] = add_pair<T>(pk[t4][e], psum[e & 1]);
+    }
+  st.l_part += psum[0] + psum[1];
 
   if (jn >= 0) vm_barrier<CH / 2>(); else vm_barrier<0>();  // V of this block has landed
   // O^T += V^T . P^T over 8 steps of 16 keys. B element e of lane (q, half)
@@ -120,10 +130,9 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const int t4 = u >> 1, hh = u & 1;
-    uint32_t pk[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) pk[e] = pack2<T>(s[t4][8 * hh + 2 * e], s[t4][8 * hh + 2 * e + 1]);
-    const typename T::vec8 pb = __builtin_bit_cast(typename T::vec8, pk);
+    const uint4 pu = make_uint4(pk[t4][4 * hh], pk[t4][4 * hh + 1], pk[t4][4 * hh + 2],
+                                pk[t4][4 * hh + 3]);
+    const typename T::vec8 pb = __builtin_bit_cast(typename T::vec8, pu);
     const int r1 = 16 * u + tr_row;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
@@ -177,18 +186,28 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
   const uint16_t* kbase = a.k + t0 * a.kst + static_cast<int64_t>(kvh) * a.khs;
   const uint16_t* vbase = a.v + t0 * a.vst + static_cast<int64_t>(kvh) * a.vhs;
 
-  // Q^T as MFMA B operand: lane (query l32, dims 16 s + 8 half .. +7); loaded
-  // before the first K/V tiles so the first K wait also covers it
+  // Q^T as MFMA B operand (lane: query l32, dims 16 s + 8 half .. +7), waited
+  // for here, before any tile load is in flight: vector memory operations
+  // complete in issue order, so a compiler wait for a register load inside the
+  // block loop would also wait for every tile load issued before it. The loop
+  // therefore issues no register loads; list entries come through the scalar
+  // cache.
   typename T::vec8 qb[KS];
   {
     const uint16_t* qp = a.q + (t0 + qg) * a.qst + static_cast<int64_t>(h) * a.qhs + 8 * half;
+    u32x4 u[KS];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qb[s] = as_vec8<T>(qvalid ? ld16(qp + 16 * s) : zero4());
+    for (int s = 0; s < KS; ++s) u[s] = __builtin_bit_cast(u32x4, qvalid ? ld16(qp + 16 * s) : zero4());
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      asm volatile("" : "+v"(u[s]));
+      qb[s] = as_vec8<T>(__builtin_bit_cast(uint4, u[s]));
+    }
   }
+  auto list_at = [&](int n) { return min(max(sld(list + n), 0), i); };
   TileLanes<D> tk, tv;
   tk.init(a.kst, w, lane);
   tv.init(a.vst, w, lane);
-  auto list_at = [&](int n) { return min(max(list[n], 0), i); };
   if (ncnt > 0) {
     const int j0 = list_at(0);
     issue_tile<D>(sk, kbase, a.kst, tk, j0, L, w, lane);

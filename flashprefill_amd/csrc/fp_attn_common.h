@@ -55,6 +55,28 @@ __device__ __forceinline__ uint32_t pack2<F16>(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
 }
 
+// p.x + p.y + acc for a packed pair of the input type (v_dot2c_f32_* against
+// (1, 1), fp32 accumulate): the row sums of the P that P.V consumes, one VALU
+// instruction per two scores
+template <typename T>
+__device__ __forceinline__ float add_pair(uint32_t p, float acc);
+template <>
+__device__ __forceinline__ float add_pair<BF16>(uint32_t p, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p), bf16x2{1.0, 1.0}, acc,
+                                         false);
+}
+template <>
+__device__ __forceinline__ float add_pair<F16>(uint32_t p, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p), f16x2{1.0, 1.0}, acc, false);
+}
+
+// Conditional rescaling: the running maximum m that P = exp2(s * scale - m)
+// is taken against moves only when a tile's maximum exceeds it by more than
+// this many log2 units, so P <= 2^kRescaleSlack. The output accumulators are
+// rescaled only then (about once per row instead of in most steps). O and l
+// are scaled by the same factors, so O / l is unchanged up to rounding.
+constexpr float kRescaleSlack = 8.0f;
+
 // wait for this wave's vector-memory ops down to N outstanding, then barrier
 template <int N>
 __device__ __forceinline__ void vm_barrier() {

@@ -38,7 +38,7 @@
 // Numerics: the reference loop with a 64-key tile — m = -inf and l = 1.0 at
 // row start, alpha = exp2(m_old - m_new) with NaN -> 1, l accumulates the fp32
 // p, P is rounded to the input dtype before P.V, O = acc * (1/l) — except that
-// m is the reference max of conditional rescaling (kRescaleSlack below), so P
+// m is the reference max of conditional rescaling (kRescaleSlack), so P
 // is rounded at a different scale than in the reference (rounding-level
 // differences in O).
 #include <type_traits>
@@ -47,15 +47,16 @@
 
 namespace fp {
 
-// Lane offsets of the direct-to-LDS loads of a 64-row half tile shared by two
-// waves: wave w fills 1 KB slices w*NI .. w*NI+NI-1 (4 rows each at d = 128).
-// off[p] is the lane's byte offset inside a slice whose index is p modulo the
-// swizzle period; the slice's own row offset goes into the scalar base.
-template <int D>
+// Lane offsets of the direct-to-LDS loads of a 64-row half tile shared by the
+// NW waves of a workgroup: wave w fills 1 KB slices w*NI .. w*NI+NI-1 (4 rows
+// each at d = 128). off[p] is the lane's byte offset inside a slice whose
+// index is p modulo the swizzle period; the slice's own row offset goes into
+// the scalar base.
+template <int D, int NW>
 struct WideLanes {
   static constexpr int CH = D / 8;              // 16-byte chunks per row
   static constexpr int RPW = 64 / CH;           // rows per 1 KB slice
-  static constexpr int NI = CH / 2;             // slices per wave per half tile
+  static constexpr int NI = CH / NW;            // slices per wave per half tile
   static constexpr int PER = D == 128 ? 4 : 2;  // period of swz over the slice index
   uint32_t off[PER];
   __device__ __forceinline__ void init(int64_t stride, int w, int lane) {
@@ -71,10 +72,12 @@ struct WideLanes {
 // This wave's loads of the half tile whose first row is at `base` into the LDS
 // buffer at byte address `lds`; rows at or past `nvalid` read row nvalid - 1
 // (their keys are masked).
-template <int D>
+template <int D, int NW>
 __device__ __forceinline__ void wide_tile(uint32_t lds, const uint16_t* base, int stride,
-                                          const WideLanes<D>& tl, int nvalid, int w, int lane) {
-  constexpr int CH = WideLanes<D>::CH, RPW = WideLanes<D>::RPW, NI = WideLanes<D>::NI;
+                                          const WideLanes<D, NW>& tl, int nvalid, int w,
+                                          int lane) {
+  using TL = WideLanes<D, NW>;
+  constexpr int CH = TL::CH, RPW = TL::RPW, NI = TL::NI;
   if (nvalid >= 64) {
     // one scalar base per tile; the slices' row offsets are scalar adds
     uint64_t sb = scalar_addr(base);
@@ -85,7 +88,7 @@ __device__ __forceinline__ void wide_tile(uint32_t lds, const uint16_t* base, in
     for (int q = 0; q < NI; ++q) {
       const int slot = w * NI + q;
       dma16_sbase_m0(lds + slot * 1024, sb + static_cast<uint64_t>(slot * RPW * stride) * 2,
-                     tl.off[q % WideLanes<D>::PER]);
+                     tl.off[q % TL::PER]);
     }
   } else {
 #pragma unroll
@@ -99,22 +102,19 @@ __device__ __forceinline__ void wide_tile(uint32_t lds, const uint16_t* base, in
   }
 }
 
-// Conditional rescaling: the running maximum m that P = exp2(s * scale - m)
-// is taken against moves only when a tile's maximum exceeds it by more than
-// this many log2 units, so P <= 2^kRescaleSlack. Rescaling the 128 AGPR-held
-// output accumulators costs three VALU instructions per element; with this
-// slack it happens about once per row instead of in most steps. O and l are
-// scaled by the same factors, so O / l is unchanged up to rounding.
-constexpr float kRescaleSlack = 8.0f;
-
-template <typename T, int D>
-__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1)))
+// QT 32-query MFMA column tiles per wave; NW = 4 / QT waves per workgroup
+// share the row's 128 queries and its K / V tiles. QT = 2: one wave per SIMD
+// (the O, S and Q^T registers of two query tiles need the AGPRs); QT = 1: two
+// waves per SIMD, everything in VGPRs.
+template <typename T, int D, int QT>
+__global__ __launch_bounds__(256 / QT) __attribute__((amdgpu_waves_per_eu(3 - QT, 3 - QT)))
 void k_attn_wide(AttnArgs a) {
+  constexpr int NW = 4 / QT;   // waves per workgroup
   constexpr int CH = D / 8;   // 16-byte chunks per key row
   constexpr int KS = D / 16;  // MFMA k-steps over the head dim
   constexpr int DT = D / 32;  // 32-row tiles of O^T
   constexpr int HT = 64 * CH;  // uint4 per half tile
-  constexpr int NI = WideLanes<D>::NI;
+  constexpr int NI = WideLanes<D, NW>::NI;
   constexpr uint32_t TB = HT * 16;  // bytes per half tile
   __shared__ uint4 sk[2][HT];
   __shared__ uint4 sv[2][HT];
@@ -144,8 +144,8 @@ void k_attn_wide(AttnArgs a) {
 
   if (ncnt == 0) {  // no block selected: m = -inf, l = 1, O = 0
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      const int qg = i * kBlock + 64 * w + 32 * qt + l32;
+    for (int qt = 0; qt < QT; ++qt) {
+      const int qg = i * kBlock + 32 * (QT * w + qt) + l32;
       if (qg < L) {
         uint16_t* op = a.o + (rec.t0 + qg) * a.ost + static_cast<int64_t>(h) * a.ohs;
 #pragma unroll
@@ -160,10 +160,10 @@ void k_attn_wide(AttnArgs a) {
   // before any tile load is in flight
   int chunk = 0;
   int listv = lane < ncnt ? list[lane] : 0;
-  typename T::vec8 qb[2][KS];
+  typename T::vec8 qb[QT][KS];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const int qg = i * kBlock + 64 * w + 32 * qt + l32;
+  for (int qt = 0; qt < QT; ++qt) {
+    const int qg = i * kBlock + 32 * (QT * w + qt) + l32;
     const bool qvalid = qg < L;
     const uint16_t* qp = a.q + (rec.t0 + qg) * a.qst + static_cast<int64_t>(h) * a.qhs + 8 * half;
     u32x4 u[KS];
@@ -172,7 +172,7 @@ void k_attn_wide(AttnArgs a) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       asm volatile("" : "+v"(u[s]));
-      asm volatile("" : "+a"(u[s]));  // B operands are read from AGPRs
+      if constexpr (QT == 2) asm volatile("" : "+a"(u[s]));  // B operands are read from AGPRs
       qb[qt][s] = as_vec8<T>(__builtin_bit_cast(uint4, u[s]));
     }
   }
@@ -185,13 +185,16 @@ void k_attn_wide(AttnArgs a) {
       asm volatile("" : "+v"(ln));  // address formed here, not held across the row
       const int e = (n & ~63) + ln;
       listv = e < ncnt ? list[e] : 0;
+      // waited for here: a wait at the readlane below would sit in every step
+      // and drain the tile loads in flight
+      asm volatile("" : "+v"(listv));
     }
     return min(max(__builtin_amdgcn_readlane(listv, n & 63), 0), i);
   };
   const bool diag_last = min(max(sld(list + ncnt - 1), 0), i) == i;
   const int nsteps = 2 * ncnt;  // half tiles of the row
 
-  WideLanes<D> tk, tv;
+  WideLanes<D, NW> tk, tv;
   tk.init(a.kst, w, lane);
   tv.init(a.vst, w, lane);
   const uint32_t sk0 = lds_addr(&sk[0][0]), sv0 = lds_addr(&sv[0][0]);
@@ -212,25 +215,30 @@ void k_attn_wide(AttnArgs a) {
   auto load_k = [&](int s, int jb) {
     int row0, rows;
     tile_rows(s, jb, row0, rows);
-    wide_tile<D>(sk0 + (s & 1) * TB, kbase + static_cast<int64_t>(row0) * a.kst, kst, tk, rows,
-                 w, lane);
+    wide_tile<D, NW>(sk0 + (s & 1) * TB, kbase + static_cast<int64_t>(row0) * a.kst, kst, tk,
+                     rows, w, lane);
   };
   auto load_v = [&](int s, int jb) {
     int row0, rows;
     tile_rows(s, jb, row0, rows);
-    wide_tile<D>(sv0 + (s & 1) * TB, vbase + static_cast<int64_t>(row0) * a.vst, vst, tv, rows,
-                 w, lane);
+    wide_tile<D, NW>(sv0 + (s & 1) * TB, vbase + static_cast<int64_t>(row0) * a.vst, vst, tv,
+                     rows, w, lane);
   };
 
   const int g16 = lane >> 4, i16 = lane & 15;
   const int tr_row = 4 * (g16 >> 1) + (i16 >> 2);
   const int tr_col = 16 * (g16 & 1) + 4 * (i16 & 3);
 
-  f32x16 o[DT][2];
+  f32x16 o[DT][QT];
+  float m_cur[QT], alpha_cur[QT], l_part[QT];
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) o[dt][0] = o[dt][1] = f32x16{};
-  float m_cur[2], alpha_cur[2], l_part[2];
-  l_part[0] = l_part[1] = half == 0 ? 1.0f : 0.0f;  // the two halves' partial sums add up to l
+  for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt][qt] = f32x16{};
+    l_part[qt] = half == 0 ? 1.0f : 0.0f;  // the two halves' partial sums add up to l
+    m_cur[qt] = -INFINITY;
+    alpha_cur[qt] = 1.0f;
+  }
 
   // block of the latest K and V tile loads
   int jk = lookup(0), jv = jk;
@@ -240,42 +248,42 @@ void k_attn_wide(AttnArgs a) {
   load_v(1, -1);
   load_k(1, jk);
 
-  float ps[2][2] = {{0.0f, 0.0f}, {0.0f, 0.0f}};  // row sums of the P being formed
+  float ps[QT][2];  // row sums of the P being formed
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) ps[qt][0] = ps[qt][1] = 0.0f;
   // P as the B operands of the four P.V k-steps. Entries of k-steps 0/1 are
   // rewritten (for S(t)) after the P.V MFMAs of step t-1 that read them have
   // issued, entries of k-steps 2/3 in the next step's block 1, so one buffer
   // serves both steps.
-  uint32_t pk[2][4][4];
+  uint32_t pk[QT][4][4];
   // S accumulators: key tile kt = 1 of S(t) stays here until block 1 of step
   // t+1 has read it, right before that block's kt = 1 MFMAs overwrite it
-  f32x16 sacc[2][2];
+  f32x16 sacc[2][QT];
   // exp2 / row sum / pack of value pair p2 (values 2 p2, 2 p2 + 1) of key tile
   // kt, query tile qt: B operand k-step 2 kt + p2 / 4, element pair p2 % 4
   auto unit = [&](int kt, int qt, int p2, const f32x16& src) {
     const float p0 = __builtin_amdgcn_exp2f(fmaf(src[2 * p2], c, -m_cur[qt]));
     const float p1 = __builtin_amdgcn_exp2f(fmaf(src[2 * p2 + 1], c, -m_cur[qt]));
-    ps[qt][0] += p0;
-    ps[qt][1] += p1;
     uint32_t& dst = pk[qt][2 * kt + (p2 >> 2)][p2 & 3];
     dst = pack2<T>(p0, p1);
+    float& acc = ps[qt][p2 & 1];
+    acc = add_pair<T>(dst, acc);  // l adds the rounded P that P.V consumes
     // computed here, in the MFMA block it is interleaved with, not sunk to
     // the P.V MFMAs that read it
-    asm volatile("" : "+v"(dst), "+v"(ps[qt][0]), "+v"(ps[qt][1]));
+    asm volatile("" : "+v"(dst), "+v"(acc));
   };
   // key > query on the diagonal block (half tile hf, key tile kt)
   auto mask = [&](f32x16& x, int hf, int kt, int qt) {
-    // key 64 hf + 32 kt + 8 (v / 4) + 4 half + v % 4 > query 64 w + 32 qt + l32,
+    // key 64 hf + 32 kt + 8 (v / 4) + 4 half + v % 4 > query 32 (QT w + qt) + l32,
     // with the lane part moved to the right so the key constants stay immediates;
     // the lane terms are recomputed here rather than held across the row
     int ln = lane;
     asm volatile("" : "+v"(ln));
-    const int lim = 64 * w + 32 * qt + (ln & 31) - 64 * hf - 4 * (ln >> 5) - 32 * kt;
+    const int lim = 32 * (QT * w + qt) + (ln & 31) - 64 * hf - 4 * (ln >> 5) - 32 * kt;
 #pragma unroll
     for (int v = 0; v < 16; ++v)
       if (8 * (v >> 2) + (v & 3) > lim) x[v] = -INFINITY;
   };
-  m_cur[0] = m_cur[1] = -INFINITY;
-  alpha_cur[0] = alpha_cur[1] = 1.0f;
 
   // step t: S(t) (HS), P.V of step t-1 (HP), S(t) on the diagonal block (CD),
   // S(t-1) on the diagonal block (PCD). The flags are compile-time constants
@@ -292,13 +300,16 @@ void k_attn_wide(AttnArgs a) {
     // MFMAs of block 2.
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(2 * NI) : "memory");
     if (HP) {  // O *= alpha(t-1), between P.V(t-2) and P.V(t-1)
-      if (__ballot(alpha_cur[0] != 1.0f || alpha_cur[1] != 1.0f)) {
+      bool moved = false;
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) moved = moved || alpha_cur[qt] != 1.0f;
+      if (__ballot(moved)) {
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-          for (int qt = 0; qt < 2; ++qt) {
-            // the accumulators are read out only on this (rare) path
-            asm volatile("" : "+a"(o[dt][qt]));
+          for (int qt = 0; qt < QT; ++qt) {
+            // AGPR-held accumulators are read out only on this (rare) path
+            if constexpr (QT == 2) asm volatile("" : "+a"(o[dt][qt]));
             o[dt][qt] *= alpha_cur[qt];
           }
       }
@@ -313,10 +324,10 @@ void k_attn_wide(AttnArgs a) {
         const int r = 32 * kt + l32;
         return skb[r * CH + ((2 * ks + half) ^ swz<D>(r))];
       };
-      f32x16 old1[2];
+      f32x16 old1[QT];
       if (HP) {
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
+        for (int qt = 0; qt < QT; ++qt) {
           old1[qt] = sacc[1][qt];
           asm volatile("" : "+v"(old1[qt]));  // read out of the accumulators here
         }
@@ -325,29 +336,31 @@ void k_attn_wide(AttnArgs a) {
       for (int kt = 0; kt < 2; ++kt) {
         uint4 ka[2];
         if (HS) {
-          sacc[kt][0] = sacc[kt][1] = f32x16{};
+#pragma unroll
+          for (int qt = 0; qt < QT; ++qt) sacc[kt][qt] = f32x16{};
           ka[0] = read_k(0, kt);
         }
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
           if (HS) {
             if (ks + 1 < KS) ka[(ks + 1) & 1] = read_k(ks + 1, kt);
-            sacc[kt][0] = T::mfma32(as_vec8<T>(ka[ks & 1]), qb[0][ks], sacc[kt][0]);
-            sacc[kt][1] = T::mfma32(as_vec8<T>(ka[ks & 1]), qb[1][ks], sacc[kt][1]);
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt)
+              sacc[kt][qt] = T::mfma32(as_vec8<T>(ka[ks & 1]), qb[qt][ks], sacc[kt][qt]);
           }
           if (kt == 0 && ks == 0) load_v(t, HS ? jv : -1);  // V(t), between MFMAs
           __builtin_amdgcn_sched_barrier(0);
           if (HP) {
             if (kt == 0 && ks == 0) {
               if (PCD) {
-                mask(old1[0], (t - 1) & 1, 1, 0);
-                mask(old1[1], (t - 1) & 1, 1, 1);
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) mask(old1[qt], (t - 1) & 1, 1, qt);
               }
             }
-            // 16 units over the 2 * KS k-steps of this block
+            // 8 QT units over the 2 * KS k-steps of this block
 #pragma unroll
-            for (int x = (16 * (kt * KS + ks)) / (2 * KS); x < (16 * (kt * KS + ks + 1)) / (2 * KS);
-                 ++x)
+            for (int x = (8 * QT * (kt * KS + ks)) / (2 * KS);
+                 x < (8 * QT * (kt * KS + ks + 1)) / (2 * KS); ++x)
               unit(1, x >> 3, x & 7, old1[x >> 3]);
           }
           __builtin_amdgcn_sched_barrier(0);
@@ -356,7 +369,7 @@ void k_attn_wide(AttnArgs a) {
     }
     if (HP) {  // l(t-1) = l(t-2) * alpha(t-1) + rowsum(P(t-1))
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
+      for (int qt = 0; qt < QT; ++qt) {
         l_part[qt] = l_part[qt] * alpha_cur[qt] + (ps[qt][0] + ps[qt][1]);
         ps[qt][0] = ps[qt][1] = 0.0f;
       }
@@ -386,8 +399,8 @@ void k_attn_wide(AttnArgs a) {
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) va[dt] = read_v(0, dt);
       }
-      f32x16 s0[2];  // key tile 0 of S(t), in VGPRs
-      float mx[2];
+      f32x16 s0[QT];  // key tile 0 of S(t), in VGPRs
+      float mx[QT];
       // VALU work of S(t), one piece after each pair of P.V MFMAs: k-step 0 of
       // the P.V loop reads and maxes key tile 0, k-step 1 key tile 1 (then
       // m(t), alpha(t)), k-steps 2 and 3 run the units of key tile 0
@@ -425,16 +438,18 @@ void k_attn_wide(AttnArgs a) {
           unit(0, j >> 2, 4 * (u - 2) + (j & 3), s0[j >> 2]);
         }
       };
+      constexpr int TPD = (4 * QT + DT - 1) / DT;  // most tasks after one dt
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int nt = u < 2 ? 4 : 8;  // tasks of this k-step
+        const int nt = u < 2 ? 2 * QT : 4 * QT;  // tasks of this k-step
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
           if (HP) {
-            const typename T::vec8 pb0 = __builtin_bit_cast(typename T::vec8, pk[0][u]);
-            const typename T::vec8 pb1 = __builtin_bit_cast(typename T::vec8, pk[1][u]);
-            o[dt][0] = T::mfma32(as_vec8<T>(va[dt]), pb0, o[dt][0]);
-            o[dt][1] = T::mfma32(as_vec8<T>(va[dt]), pb1, o[dt][1]);
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+              const typename T::vec8 pb = __builtin_bit_cast(typename T::vec8, pk[qt][u]);
+              o[dt][qt] = T::mfma32(as_vec8<T>(va[dt]), pb, o[dt][qt]);
+            }
             if (u + 1 < 4) va[dt] = read_v(u + 1, dt);
           }
           if (u == 0 && dt == 0 && HS) load_k(t + 2, t + 2 < nsteps ? jk : -1);
@@ -443,7 +458,7 @@ void k_attn_wide(AttnArgs a) {
             // tasks nt * dt / DT .. nt * (dt + 1) / DT - 1, as a loop of
             // constant trip count so that it unrolls completely
 #pragma unroll
-            for (int k = 0; k < 8 / DT; ++k) {
+            for (int k = 0; k < TPD; ++k) {
               const int j = (nt * dt) / DT + k;
               if (j < (nt * (dt + 1)) / DT) task(u, j);
             }
@@ -469,8 +484,8 @@ void k_attn_wide(AttnArgs a) {
   int ln = lane;
   asm volatile("" : "+v"(ln));  // output addresses formed here, not held across the row
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const int qg = i * kBlock + 64 * w + 32 * qt + (ln & 31);
+  for (int qt = 0; qt < QT; ++qt) {
+    const int qg = i * kBlock + 32 * (QT * w + qt) + (ln & 31);
     const float rcp = 1.0f / pair32_sum(l_part[qt]);
     if (qg < L) {
       uint16_t* op = a.o + (rec.t0 + qg) * a.ost + static_cast<int64_t>(h) * a.ohs;
@@ -488,18 +503,28 @@ void k_attn_wide(AttnArgs a) {
   }
 }
 
-hipError_t launch_attn_wide(const AttnArgs& a, int dtype, int head_dim, int64_t grid,
-                            hipStream_t s) {
+template <int QT>
+hipError_t launch_qt(const AttnArgs& a, int dtype, int head_dim, int64_t grid, hipStream_t s) {
   if (grid <= 0) return hipSuccess;
-  const dim3 g(static_cast<unsigned>(grid)), blk(128);
+  const dim3 g(static_cast<unsigned>(grid)), blk(256 / QT);
   if (dtype == FP_DTYPE_BF16) {
-    if (head_dim == 128) hipLaunchKernelGGL((k_attn_wide<BF16, 128>), g, blk, 0, s, a);
-    else hipLaunchKernelGGL((k_attn_wide<BF16, 64>), g, blk, 0, s, a);
+    if (head_dim == 128) hipLaunchKernelGGL((k_attn_wide<BF16, 128, QT>), g, blk, 0, s, a);
+    else hipLaunchKernelGGL((k_attn_wide<BF16, 64, QT>), g, blk, 0, s, a);
   } else {
-    if (head_dim == 128) hipLaunchKernelGGL((k_attn_wide<F16, 128>), g, blk, 0, s, a);
-    else hipLaunchKernelGGL((k_attn_wide<F16, 64>), g, blk, 0, s, a);
+    if (head_dim == 128) hipLaunchKernelGGL((k_attn_wide<F16, 128, QT>), g, blk, 0, s, a);
+    else hipLaunchKernelGGL((k_attn_wide<F16, 64, QT>), g, blk, 0, s, a);
   }
   return hipGetLastError();
+}
+
+hipError_t launch_attn_wide(const AttnArgs& a, int dtype, int head_dim, int64_t grid,
+                            hipStream_t s) {
+  return launch_qt<2>(a, dtype, head_dim, grid, s);
+}
+
+hipError_t launch_attn_pipe(const AttnArgs& a, int dtype, int head_dim, int64_t grid,
+                            hipStream_t s) {
+  return launch_qt<1>(a, dtype, head_dim, grid, s);
 }
 
 }  // namespace fp

@@ -116,6 +116,7 @@ int attn_impl() {
   const char* e = getenv("FLASHPREFILL_ATTN");
   if (e && strcmp(e, "persistent") == 0) return 2;
   if (e && strcmp(e, "wide") == 0) return 3;
+  if (e && strcmp(e, "pipe") == 0) return 4;
   return 1;
 }
 
@@ -266,6 +267,9 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
                         static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap, s);
   } else if (impl == 3) {
     e = fp::launch_attn_wide(a, p->dtype, p->head_dim,
+                             static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap, s);
+  } else if (impl == 4) {
+    e = fp::launch_attn_pipe(a, p->dtype, p->head_dim,
                              static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap, s);
   } else {
     int cus = 0;

@@ -69,6 +69,8 @@ hipError_t launch_search(const SearchArgs& a, int dtype, int head_dim, int64_t g
 hipError_t launch_attn(const AttnArgs& a, int dtype, int head_dim, int64_t grid, hipStream_t s);
 hipError_t launch_attn_wide(const AttnArgs& a, int dtype, int head_dim, int64_t grid,
                             hipStream_t s);
+hipError_t launch_attn_pipe(const AttnArgs& a, int dtype, int head_dim, int64_t grid,
+                            hipStream_t s);
 hipError_t launch_attn_pp(const AttnArgs& a, int dtype, int head_dim, int num_wg, hipStream_t s);
 
 }  // namespace fp

@@ -24,7 +24,7 @@ def attn_key_tile() -> int:
     kernel (FLASHPREFILL_ATTN=persistent) and the 64-queries-per-wave kernel
     (FLASHPREFILL_ATTN=wide)."""
     import os
-    return 64 if os.environ.get("FLASHPREFILL_ATTN") in ("persistent", "wide") else 128
+    return 64 if os.environ.get("FLASHPREFILL_ATTN") in ("persistent", "wide", "pipe") else 128
 
 
 def _dtype_code(t: torch.Tensor) -> int:

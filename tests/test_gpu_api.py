@@ -80,7 +80,7 @@ def test_all_blocks_selected_is_dense_causal():
     _close(o, ref.permute(1, 0, 2))
 
 
-@pytest.mark.parametrize("kernel", ["rows", "persistent", "wide"])
+@pytest.mark.parametrize("kernel", ["rows", "persistent", "wide", "pipe"])
 def test_all_blocks_selected_long_rows(kernel, monkeypatch):
     # 8300 tokens: 65 blocks per row (the wide kernel reloads its 64-entry
     # block-list chunk), a partial last block of 108 rows (its second half tile

@@ -22,7 +22,7 @@ pytestmark = pytest.mark.gpu
 
 # the attention kernels: one workgroup per row (default), the persistent one and
 # the 64-queries-per-wave one
-KERNELS = ["rows", "persistent", "wide"]
+KERNELS = ["rows", "persistent", "wide", "pipe"]
 
 
 @pytest.fixture(params=KERNELS)
