@@ -47,14 +47,20 @@ struct AttnState {
 };
 
 // One selected block: S = K.Q^T, online softmax, O += V^T.P^T, and the
-// pipelined refills of the K / V buffers with block `jn` (when jn >= 0).
+// pipelined refills of the K / V buffers with block `jn` (when jn >= 0). The
+// list entry at `pf` (the block after jn, or any valid entry) is read into
+// `jpf` right after the K refill is issued, unclamped: the scalar load then
+// completes behind the softmax, which reads no LDS, instead of stalling the
+// next block (scalar loads share the LDS wait counter, so the compiler waits
+// for them at the first LDS read after them).
 template <typename T, int D, bool DIAG>
 __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T::vec8* qb,
                                            const uint4* sk, uint4* sk_w, const uint16_t* sv16,
                                            uint4* sv_w, const uint16_t* kbase,
                                            const uint16_t* vbase, int64_t kst, int64_t vst,
                                            const TileLanes<D>& tk, const TileLanes<D>& tv,
-                                           int jn, int L, float c, int w, int lane) {
+                                           int jn, const int32_t* pf, int& jpf, int L, float c,
+                                           int w, int lane) {
   constexpr int CH = D / 8;
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
@@ -75,6 +81,7 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
   }
   lds_barrier();  // every wave is done with the K buffer
   if (jn >= 0) issue_tile<D>(sk_w, kbase, kst, tk, jn, L, w, lane);
+  jpf = sld(pf);
 
   if constexpr (DIAG) {  // key > query is masked on the diagonal block
 #pragma unroll
@@ -90,8 +97,7 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
   for (int t4 = 0; t4 < 4; ++t4)
 #pragma unroll
     for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[t4][v]);
-  mx = fmaxf(mx, xor32_f(mx));
-  const float m_tile = mx * c;
+  const float m_tile = pair32_max(mx) * c;
   // the running max moves (and O, l are rescaled) only when some row of the
   // wave exceeds it by more than kRescaleSlack; always on the row's first block
   if (__ballot(m_tile > st.m_run + kRescaleSlack)) {
@@ -224,16 +230,21 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
   // the diagonal block, when selected, is the last entry of the ascending list
   const bool has_diag = ncnt > 0 && list_at(ncnt - 1) == i;
   const int nplain = ncnt - (has_diag ? 1 : 0);
+  // block n refills the buffers with entry n + 1 and prefetches entry n + 2
+  // (entry ncnt - 1 past the end of the list; not used then)
+  int jraw = ncnt > 1 ? sld(list + 1) : 0;
   for (int n = 0; n < nplain; ++n) {
-    const int jn = n + 1 < ncnt ? list_at(n + 1) : -1;
-    attn_block<T, D, false>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv, jn, L,
-                            c, w, lane);
+    const int jn = n + 1 < ncnt ? min(max(jraw, 0), i) : -1;
+    attn_block<T, D, false>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv, jn,
+                            list + min(n + 2, ncnt - 1), jraw, L, c, w, lane);
   }
-  if (has_diag)
-    attn_block<T, D, true>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv, -1, L, c,
-                           w, lane);
+  if (has_diag) {
+    int unused;
+    attn_block<T, D, true>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv, -1,
+                           list, unused, L, c, w, lane);
+  }
 
-  const float l = st.l_part + xor32_f(st.l_part);
+  const float l = pair32_sum(st.l_part);
   const float rcp = 1.0f / l;
   if (qvalid) {
     uint16_t* op = a.o + (t0 + qg) * a.ost + static_cast<int64_t>(h) * a.ohs;
