@@ -67,7 +67,8 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
   const int half = lane >> 5, l32 = lane & 31;
   const int qrow = 32 * w + l32;
 
-  vm_barrier<CH / 2>();  // K of this block has landed (V may still be in flight)
+  // entered with K of this block landed in every wave's part and the barrier
+  // passed (V may still be in flight)
   f32x16 s[4];
 #pragma unroll
   for (int t4 = 0; t4 < 4; ++t4) {
@@ -152,8 +153,13 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
       st.o[dt] = T::mfma32(as_vec8<T>(va), pb, st.o[dt]);
     }
   }
-  lds_barrier();  // every wave is done with the V buffer
-  if (jn >= 0) issue_tile<D>(sv_w, vbase, vst, tv, jn, L, w, lane);
+  if (jn >= 0) {
+    // one barrier for two conditions: every wave is done with the V buffer,
+    // and every wave's part of the next block's K (the only load in flight)
+    // has landed, so the next block starts right after the V refill
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    issue_tile<D>(sv_w, vbase, vst, tv, jn, L, w, lane);
+  }
 }
 
 template <typename T, int D>
@@ -218,6 +224,7 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
     const int j0 = list_at(0);
     issue_tile<D>(sk, kbase, a.kst, tk, j0, L, w, lane);
     issue_tile<D>(sv, vbase, a.vst, tv, j0, L, w, lane);
+    vm_barrier<CH / 2>();  // K of the first block has landed
   }
 
   AttnState<T, D> st;
