@@ -198,12 +198,21 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
   const uint16_t* kbase = a.k + t0 * a.kst + static_cast<int64_t>(kvh) * a.khs;
   const uint16_t* vbase = a.v + t0 * a.vst + static_cast<int64_t>(kvh) * a.vhs;
 
-  // Q^T as MFMA B operand (lane: query l32, dims 16 s + 8 half .. +7), waited
-  // for here, before any tile load is in flight: vector memory operations
-  // complete in issue order, so a compiler wait for a register load inside the
-  // block loop would also wait for every tile load issued before it. The loop
-  // therefore issues no register loads; list entries come through the scalar
-  // cache.
+  auto list_at = [&](int n) { return min(max(sld(list + n), 0), i); };
+  TileLanes<D> tk, tv;
+  tk.init(a.kst, w, lane);
+  tv.init(a.vst, w, lane);
+  if (ncnt > 0) {
+    const int j0 = list_at(0);
+    issue_tile<D>(sk, kbase, a.kst, tk, j0, L, w, lane);
+    issue_tile<D>(sv, vbase, a.vst, tv, j0, L, w, lane);
+  }
+  // Q^T as MFMA B operand (lane: query l32, dims 16 s + 8 half .. +7), loaded
+  // after the first block's tile loads and waited for here, so one memory
+  // latency covers both: vector memory operations complete in issue order, so
+  // this wait (and any compiler wait for a register load) also waits for every
+  // tile load issued before it. The block loop therefore issues no register
+  // loads; list entries come through the scalar cache.
   typename T::vec8 qb[KS];
   {
     const uint16_t* qp = a.q + (t0 + qg) * a.qst + static_cast<int64_t>(h) * a.qhs + 8 * half;
@@ -216,16 +225,7 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
       qb[s] = as_vec8<T>(__builtin_bit_cast(uint4, u[s]));
     }
   }
-  auto list_at = [&](int n) { return min(max(sld(list + n), 0), i); };
-  TileLanes<D> tk, tv;
-  tk.init(a.kst, w, lane);
-  tv.init(a.vst, w, lane);
-  if (ncnt > 0) {
-    const int j0 = list_at(0);
-    issue_tile<D>(sk, kbase, a.kst, tk, j0, L, w, lane);
-    issue_tile<D>(sv, vbase, a.vst, tv, j0, L, w, lane);
-    vm_barrier<CH / 2>();  // K of the first block has landed
-  }
+  if (ncnt > 0) vm_barrier<0>();  // the first block's K and V have landed
 
   AttnState<T, D> st;
 #pragma unroll

@@ -274,8 +274,7 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
         for (int rg = 0; rg < 4; ++rg)
 #pragma unroll
           for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc[rg][v]);
-        mx = fmaxf(mx, xor32_f(mx));
-        m = mx * c;
+        m = pair32_max(mx) * c;
 #pragma unroll
         for (int rg = 0; rg < 4; ++rg)
 #pragma unroll
@@ -289,8 +288,7 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
             const int row = 32 * rg + 8 * (v >> 2) + 4 * half + (v & 3);
             if (full || (diag && row == kBlock - 1)) mx = fmaxf(mx, acc[rg][v]);
           }
-        mx = fmaxf(mx, xor32_f(mx));
-        m = mx * c;
+        m = pair32_max(mx) * c;
 #pragma unroll
         for (int rg = 0; rg < 4; ++rg)
 #pragma unroll
@@ -300,7 +298,7 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
               sum += __builtin_amdgcn_exp2f(fmaf(acc[rg][v], c, -m));
           }
       }
-      sum += xor32_f(sum);
+      sum = pair32_sum(sum);
       if (half == 0 && jv) {
         pl[j] = sum;
         ml[j] = m;
