@@ -45,9 +45,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="time budget of the CPU baseline sample")
     ap.add_argument("--collect-traffic", action="store_true",
-                    help="measure the attention kernel's HBM bytes per launch with two "
-                         "rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE), calibrated on a "
-                         "copy kernel, and write the summary under profiles/")
+                    help="measure the attention, pooling and search kernels' bytes per "
+                         "launch beyond L2 with two rocprofv3 --pmc passes (read and write "
+                         "request counts by size, checked on a 1 GiB copy), and write the "
+                         "summaries under profiles/")
     ap.add_argument("--traffic-probe", action="store_true",
                     help=argparse.SUPPRESS)  # child of --collect-traffic: one attention + one copy
     return ap.parse_args()
@@ -67,7 +68,7 @@ def timed(fn, reps, stream=None):
     return s.elapsed_time(e) / reps
 
 
-COPY_BYTES = 1 << 30  # calibration copy: 1 GiB read + 1 GiB written
+COPY_BYTES = 1 << 30  # check copy: 1 GiB read + 1 GiB written
 
 
 def attn_kernel_name():
@@ -105,11 +106,33 @@ def traffic_probe(args):
     print("traffic probe done", flush=True)
 
 
+# L2 -> fabric request counters of one pass each (at most 4 TCC counters per
+# pass). On gfx950 with this ROCm, reads leave L2 as 128-byte requests that
+# FETCH_SIZE counts as 64 bytes (its 128-byte term, TCC_BUBBLE, reads 0: a
+# kernel reading exactly 1 GiB with coalesced 16-byte loads reports 0.5 GiB),
+# so read bytes come from the raw counts; writes are 64-byte requests, which
+# WRITE_SIZE counts correctly.
+TRAFFIC_PASSES = {
+    "read": ["TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum"],
+    "write": ["TCC_EA0_WRREQ_sum", "TCC_EA0_WRREQ_64B_sum"],
+}
+
+
+def traffic_bytes(kind, c):
+    """Bytes from one dispatch's counters (dict name -> value)."""
+    if kind == "read":
+        n, n32, n64 = c["TCC_EA0_RDREQ_sum"], c["TCC_EA0_RDREQ_32B_sum"], c["TCC_EA0_RDREQ_64B_sum"]
+        return 32.0 * n32 + 64.0 * n64 + 128.0 * (n - n32 - n64)
+    n, n64 = c["TCC_EA0_WRREQ_sum"], c["TCC_EA0_WRREQ_64B_sum"]
+    return 32.0 * (n - n64) + 64.0 * n64
+
+
 def collect_traffic(args):
     """Two rocprofv3 counter passes over --traffic-probe (started as child
-    processes; this process never touches the GPU). FETCH_SIZE / WRITE_SIZE
-    of the attention, pooling and search dispatches are scaled by (known
-    bytes / counter reading) of the copy kernel in the same pass."""
+    processes; this process never touches the GPU): L2 -> fabric read and
+    write request counts of the attention, pooling and search dispatches,
+    converted to bytes by request size. The 1 GiB copy in the same pass is
+    the check: its read and write bytes must come out at 1 GiB each."""
     import csv
     import glob
     import subprocess
@@ -117,14 +140,15 @@ def collect_traffic(args):
     probe = [sys.executable, "-u", os.path.abspath(__file__), "--traffic-probe",
              "--seq-len", str(args.seq_len), "--seed", str(args.seed), "--alpha", str(args.alpha)]
     res = {}
-    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+    for kind, ctrs in TRAFFIC_PASSES.items():
         with tempfile.TemporaryDirectory() as td:
-            cmd = ["rocprofv3", "--pmc", ctr, "--output-format", "csv", "-d", td, "-o", "p", "--"] + probe
+            cmd = ["rocprofv3", "--pmc"] + ctrs + ["--output-format", "csv", "-d", td, "-o", "p",
+                                                   "--"] + probe
             print("bench: " + " ".join(cmd), file=sys.stderr, flush=True)
             r = subprocess.run(["timeout", "-s", "KILL", "300"] + cmd, capture_output=True, text=True)
             if r.returncode != 0:
-                raise SystemExit(f"rocprofv3 pass {ctr} failed ({r.returncode}): {r.stderr[-800:]}")
-            vals = {}
+                raise SystemExit(f"rocprofv3 pass {kind} failed ({r.returncode}): {r.stderr[-800:]}")
+            disp = {}  # (stage, dispatch id) -> {counter: value}
             for f in glob.glob(f"{td}/**/*counter_collection.csv", recursive=True):
                 for row in csv.DictReader(open(f)):
                     name = row["Kernel_Name"]
@@ -132,44 +156,43 @@ def collect_traffic(args):
                            "pool" if "fp::k_pool<" in name else
                            "search" if "fp::k_search<" in name else
                            "copy" if "copy" in name.lower() else None)
-                    if key is None or row["Counter_Name"] != ctr:
+                    if key is None or row["Counter_Name"] not in ctrs:
                         continue
-                    vals.setdefault(key, []).append(float(row["Counter_Value"]))
-            if "attn" not in vals or "copy" not in vals:
-                raise SystemExit(f"counter {ctr}: dispatches not found ({sorted(vals)})")
-            # FETCH_SIZE / WRITE_SIZE are in KiB per dispatch; take the largest
-            # copy dispatch (the 1 GiB one)
-            attn_kib = vals["attn"][-1]
-            copy_kib = max(vals["copy"])
-            scale = COPY_BYTES / (copy_kib * 1024.0)
-            res[ctr] = {"attn_kib": attn_kib, "copy_kib": copy_kib, "copy_scale": scale,
-                        "attn_bytes": attn_kib * 1024.0 * scale}
-            for st in ("pool", "search"):
-                if st in vals:
-                    res[ctr][st + "_kib"] = vals[st][-1]
-                    res[ctr][st + "_bytes"] = vals[st][-1] * 1024.0 * scale
+                    d = disp.setdefault((key, int(row["Dispatch_Id"])), {})
+                    d[row["Counter_Name"]] = d.get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+            byts = {}
+            for (key, did), c in sorted(disp.items(), key=lambda x: x[0][1]):
+                if all(x in c for x in ctrs):
+                    byts.setdefault(key, []).append(traffic_bytes(kind, c))
+            if "attn" not in byts or "copy" not in byts:
+                raise SystemExit(f"pass {kind}: dispatches not found ({sorted(byts)})")
+            # the last dispatch of each stage; the probe's last copy is the 1 GiB one
+            # (earlier copy kernels are the input conversions)
+            res[kind] = {st: v[-1] for st, v in byts.items() if st != "copy"}
+            res[kind]["copy_check"] = byts["copy"][-1] / COPY_BYTES
+    rd, wr = res["read"], res["write"]
+    method = ("rocprofv3 --pmc " + " ".join(TRAFFIC_PASSES["read"]) + " (read bytes = 128 x "
+              "128-byte + 64 x 64-byte + 32 x 32-byte requests), then --pmc " +
+              " ".join(TRAFFIC_PASSES["write"]) + " (write bytes = 64 x 64-byte + 32 x 32-byte "
+              "requests), over python -u bench.py --traffic-probe")
     out = {
         "kernel": attn_kernel_name(), "workload": f"bench.py config 3, seq_len {args.seq_len}, "
         f"seed {args.seed}, alpha {args.alpha}",
-        "command": ("python bench.py --collect-traffic  (runs, per counter: rocprofv3 --pmc "
-                    "<FETCH_SIZE|WRITE_SIZE> --output-format csv -- python -u bench.py "
-                    "--traffic-probe)"),
-        "calibration": f"torch copy of {COPY_BYTES} bytes in the same pass",
-        "fetch": res["FETCH_SIZE"], "write": res["WRITE_SIZE"],
-        "traffic_bytes": res["FETCH_SIZE"]["attn_bytes"] + res["WRITE_SIZE"]["attn_bytes"],
+        "command": "python bench.py --collect-traffic", "method": method,
+        "check": {"copy_1GiB_read_ratio": rd["copy_check"], "copy_1GiB_write_ratio": wr["copy_check"]},
+        "fetch_bytes": rd["attn"], "write_bytes": wr["attn"],
+        "traffic_bytes": rd["attn"] + wr["attn"],
     }
     os.makedirs(os.path.dirname(traffic_file(args.seq_len)), exist_ok=True)
     with open(traffic_file(args.seq_len), "w") as fh:
         json.dump(out, fh, indent=1)
     print(json.dumps(out), flush=True)
-    stages = {"workload": out["workload"], "command": out["command"],
-              "calibration": out["calibration"]}
+    stages = {"workload": out["workload"], "command": out["command"], "method": method,
+              "check": out["check"]}
     for st, kern in (("pool", "k_pool"), ("search", "k_search")):
-        if f"{st}_bytes" in res["FETCH_SIZE"] and f"{st}_bytes" in res["WRITE_SIZE"]:
-            stages[kern] = {"fetch_bytes": res["FETCH_SIZE"][f"{st}_bytes"],
-                            "write_bytes": res["WRITE_SIZE"][f"{st}_bytes"],
-                            "traffic_bytes": res["FETCH_SIZE"][f"{st}_bytes"] +
-                            res["WRITE_SIZE"][f"{st}_bytes"]}
+        if st in rd and st in wr:
+            stages[kern] = {"fetch_bytes": rd[st], "write_bytes": wr[st],
+                            "traffic_bytes": rd[st] + wr[st]}
     with open(stage_traffic_file(args.seq_len), "w") as fh:
         json.dump(stages, fh, indent=1)
     print(json.dumps(stages), flush=True)
@@ -501,8 +524,8 @@ def main():
         "roofline": {"bound": "mfma", "kernel": f"fp::{attn_kernel_name()} (block-sparse attention)",
                      "achieved": round(exec_tflops, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(exec_tflops / PEAK_BF16_TFLOPS, 4),
-                     "traffic": traffic, "traffic_unit": "bytes per launch (HBM, calibrated "
-                     "FETCH_SIZE + WRITE_SIZE)", "traffic_source": traffic_src,
+                     "traffic": traffic, "traffic_unit": "bytes per launch beyond L2 (read + "
+                     "write requests by size)", "traffic_source": traffic_src,
                      "algorithmic_kv_bytes": n_exec * 2 * 128 * d * q.element_size()},
         "search_roofline": search_roofline,
         "cpu_baseline": cpu,

@@ -93,6 +93,9 @@ int layout(const fp_problem* p, fp_ws_layout* L) {
   if (Hq * cap > (int64_t(1) << 31)) return fail(FP_E_INVALID_ARG, "too many work items");
   if (Hq * tri >= (int64_t(1) << 31))
     return fail(FP_E_UNSUPPORTED, "index lists of 2^31 entries or more are not supported");
+  // the search addresses a sequence's pooled keys with 32-bit byte offsets
+  if (nb_max * Hkv * d * 2 >= (int64_t(1) << 31))
+    return fail(FP_E_UNSUPPORTED, "pooled keys of 2^31 bytes or more per sequence are not supported");
   size_t off = 0;
   L->status_off = off;     off = align_up(off + 4);
   L->seq_tile_off = off;   off = align_up(off + 8 * (B + 1));

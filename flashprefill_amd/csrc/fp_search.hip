@@ -230,14 +230,36 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
     const int half = lane >> 5, l32 = lane & 31;
     const float c = a.sm_scale_log2;
     constexpr int CH = D / 8;
+    const int64_t mk_row = static_cast<int64_t>(a.Hkv) * D;
+    // wave-uniform base of this kv head's pooled keys; the lane part of a
+    // load address is a 32-bit byte offset formed at each load
+    const char* mkb = reinterpret_cast<const char*>(a.mk + tile_b * mk_row +
+                                                    static_cast<int64_t>(kvh) * D);
+    // a sequence's pooled keys span < 2^31 bytes (checked on the host)
+    const int mk_row_b = static_cast<int>(mk_row) * 2;
+    const int ntiles = (n + 31) >> 5;
+    // pooled keys of one 32-key tile as MFMA B operands (lane: key 32 tile + l32)
+    typename T::vec8 kb[KS];
+    auto load_kb = [&](int tile) {
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int j = 32 * tile + (ln & 31);
+      const bool jv = j < n;
+      const char* p = mkb + (j * mk_row_b + 16 * (ln >> 5));
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        kb[s] = as_vec8<T>(jv ? *reinterpret_cast<const uint4*>(p + 32 * s) : zero4());
+    };
     // stage the query block in LDS with direct-to-LDS loads (rows past the
     // sequence end are then zeroed: they still count for j < i); every wave
-    // reads it as MFMA A operands (rows 32*rg + l32, dims 16*s + 8*half .. +7)
+    // reads it as MFMA A operands (rows 32*rg + l32, dims 16*s + 8*half .. +7).
+    // The wave's first key tile is loaded in the same wait.
     {
       TileLanes<D> tq;
       tq.init(a.qst, __builtin_amdgcn_readfirstlane(w), lane);
       issue_tile<D>(sq, a.q + t0 * a.qst + static_cast<int64_t>(h) * a.qhs, a.qst, tq, i, L,
                     __builtin_amdgcn_readfirstlane(w), lane);
+      if (w < ntiles) load_kb(w);
       asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
       if ((i + 1) * kBlock > L) {
         for (int cidx = t; cidx < kBlock * CH; cidx += 256)
@@ -245,16 +267,10 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
         __syncthreads();
       }
     }
-    const int64_t mk_row = static_cast<int64_t>(a.Hkv) * D;
-    const uint16_t* mkb = a.mk + tile_b * mk_row + static_cast<int64_t>(kvh) * D + 8 * half;
-    const int ntiles = (n + 31) >> 5;
     for (int tile = w; tile < ntiles; tile += 4) {
       const int j = 32 * tile + l32;
       const bool jv = j < n;
-      typename T::vec8 kb[KS];
-#pragma unroll
-      for (int s = 0; s < KS; ++s)
-        kb[s] = as_vec8<T>(jv ? ld16(mkb + static_cast<int64_t>(j) * mk_row + 16 * s) : zero4());
+      if (tile != w) load_kb(tile);
       f32x16 acc[4];
 #pragma unroll
       for (int rg = 0; rg < 4; ++rg) acc[rg] = f32x16{};
