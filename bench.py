@@ -265,6 +265,19 @@ def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines):
         call.search()
 
     ms_search = timed(search_stage, max(3, steps))
+    # the same split inside full calls: events between the search stages and
+    # the attention of each staged call (same kernels as call.run())
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(max(3, steps))]
+    torch.cuda.synchronize()
+    for e3 in ev:
+        e3[0].record()
+        search_stage()
+        e3[1].record()
+        call.attn()
+        e3[2].record()
+    torch.cuda.synchronize()
+    in_call_search = sum(e3[0].elapsed_time(e3[1]) for e3 in ev) / len(ev)
+    in_call_total = sum(e3[0].elapsed_time(e3[2]) for e3 in ev) / len(ev)
     ms_pool = timed(call.pool, max(3, steps))
     ms_score = timed(call.search, max(3, steps))
     ms_attn = timed(call.attn, max(3, steps))
@@ -278,6 +291,8 @@ def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines):
         "ms_total": ms_total, "ms_search": ms_search, "ms_attn": ms_attn,
         "ms_pool": ms_pool, "ms_score": ms_score,
         "search_share": ms_search / ms_total, "executed_blocks": n_exec,
+        "in_call_split": {"ms_search": in_call_search, "ms_total": in_call_total,
+                          "search_share": in_call_search / in_call_total},
         "density": n_exec / causal_blocks, "executed_tflops": exec_tflops,
         "mfma_frac": exec_tflops / PEAK_BF16_TFLOPS,
         "effective_tflops": dense_flops / (ms_total * 1e-3) / 1e12,
@@ -516,6 +531,7 @@ def main():
         "t_search_ms": round(ms_search, 4),
         "t_attn_ms": round(ms_attn, 4),
         "search_share": round(ms_search / ms_total, 4),
+        "search_share_in_call": round(r["in_call_split"]["search_share"], 4),
         "density": round(density, 5),
         "executed_blocks": n_exec,
         "executed_tflops": round(exec_tflops, 2),
