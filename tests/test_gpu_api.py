@@ -99,6 +99,33 @@ def test_all_blocks_selected_long_rows(kernel, monkeypatch):
     _close(o, ref.permute(1, 0, 2).cpu())
 
 
+@pytest.mark.parametrize("kernel", ["rows", "persistent", "wide", "pipe"])
+def test_growing_logits_rescale_every_block(kernel, monkeypatch):
+    # every key block's logits exceed the previous block's by ~9 log2 units
+    # (more than the kernels' rescaling slack of 8), so the running max moves
+    # and the output accumulators are rescaled on every block; the last
+    # query rows then attend almost only to their own (diagonal) block.
+    # All blocks selected (alpha 0): dense causal attention vs fp32 SDPA.
+    monkeypatch.setenv("FLASHPREFILL_ATTN", kernel)
+    T, Hq, Hkv, d = 2048, 2, 1, 128
+    g = torch.Generator().manual_seed(31)
+    e = torch.zeros(d)
+    e[0] = 1.0
+    q = (e + 0.05 * torch.randn(T, Hq, d, generator=g)).to(torch.bfloat16)
+    blk = (torch.arange(T) // 128).float()
+    k = (70.0 * blk[:, None, None] * e + torch.randn(T, Hkv, d, generator=g)).to(torch.bfloat16)
+    v = torch.randn(T, Hkv, d, generator=g).to(torch.bfloat16)
+    o = torch.empty(T, Hq, d, dtype=torch.bfloat16, device=DEV)
+    cu = torch.tensor([0, T], dtype=torch.int32, device=DEV)
+    flash_prefill_varlen_func(q.to(DEV), k.to(DEV), v.to(DEV), o, cu, T, 0.0)
+    torch.cuda.synchronize()
+    qq = q.float().permute(1, 0, 2).contiguous().to(DEV)
+    kk = k.float().permute(1, 0, 2).repeat_interleave(Hq // Hkv, 0).contiguous().to(DEV)
+    vv = v.float().permute(1, 0, 2).repeat_interleave(Hq // Hkv, 0).contiguous().to(DEV)
+    ref = torch.nn.functional.scaled_dot_product_attention(qq, kk, vv, is_causal=True)
+    _close(o, ref.permute(1, 0, 2).cpu())
+
+
 def test_status_flags_and_untouched_output():
     T, Hq, Hkv, d = 1000, 4, 1, 128
     q, k, v = _rand((T, Hq, d), 11).to(DEV), _rand((T, Hkv, d), 12).to(DEV), _rand((T, Hkv, d), 13).to(DEV)
