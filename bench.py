@@ -51,6 +51,11 @@ def parse():
                          "summaries under profiles/")
     ap.add_argument("--traffic-probe", action="store_true",
                     help=argparse.SUPPRESS)  # child of --collect-traffic: one attention + one copy
+    ap.add_argument("--power", action="store_true",
+                    help="run the attention stage back to back for --power-seconds while "
+                         "sampling socket power with amd-smi; print time, power and energy "
+                         "per launch")
+    ap.add_argument("--power-seconds", type=float, default=4.0)
     return ap.parse_args()
 
 
@@ -196,6 +201,62 @@ def collect_traffic(args):
     with open(stage_traffic_file(args.seq_len), "w") as fh:
         json.dump(stages, fh, indent=1)
     print(json.dumps(stages), flush=True)
+
+
+def power_run(args):
+    """Attention launches back to back on the bench input for --power-seconds,
+    socket power sampled every 0.2 s with `amd-smi metric -p` in a thread (a
+    child process per sample; this process owns the GPU). Median power over
+    the run (the first two samples dropped), HIP-event time per launch, and
+    their product: energy per launch."""
+    import statistics
+    import subprocess
+    import threading
+    import torch
+    from flashprefill_amd import synth
+    from flashprefill_amd.runtime import FlashPrefillCall
+    dev = torch.device("cuda:0")
+    spec = synth.llama_spec(args.seq_len, seed=args.seed)
+    q, k, v, cu = synth.make_inputs(spec, device=dev)
+    o = torch.empty_like(q)
+    call = FlashPrefillCall(q, k, v, o, cu, args.seq_len, alpha=args.alpha)
+    call.plan(); call.pool(); call.search(); call.attn()
+    torch.cuda.synchronize()
+    watts, stop = [], threading.Event()
+
+    def sample():
+        while not stop.is_set():
+            r = subprocess.run(["amd-smi", "metric", "-p", "-g", "0", "--csv"],
+                               capture_output=True, text=True)
+            rows = [ln.split(",") for ln in r.stdout.strip().splitlines() if ln]
+            if len(rows) >= 2 and "socket_power" in rows[0]:
+                try:
+                    watts.append(float(rows[1][rows[0].index("socket_power")]))
+                except ValueError:
+                    pass
+            stop.wait(0.2)
+
+    th = threading.Thread(target=sample)
+    th.start()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n, t0 = 0, time.time()
+    e0.record()
+    while time.time() - t0 < args.power_seconds:
+        for _ in range(20):
+            call.attn()
+        torch.cuda.synchronize()
+        n += 20
+    e1.record()
+    torch.cuda.synchronize()
+    stop.set()
+    th.join()
+    ms = e0.elapsed_time(e1) / n
+    w = statistics.median(watts[2:]) if len(watts) > 2 else None
+    print(json.dumps({"kernel": attn_kernel_name(), "workload": f"bench.py config 3, seq_len "
+                      f"{args.seq_len}, seed {args.seed}, alpha {args.alpha}",
+                      "launches": n, "ms_per_launch": round(ms, 4), "power_samples": len(watts),
+                      "socket_power_W_median": w,
+                      "energy_J_per_launch": round(w * ms / 1e3, 3) if w else None}), flush=True)
 
 
 def dense_causal_flops(S, Hq, d):
@@ -443,6 +504,9 @@ def main():
         return
     if args.traffic_probe:
         traffic_probe(args)
+        return
+    if args.power:
+        power_run(args)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (one MI355X per box); "
