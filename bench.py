@@ -77,7 +77,8 @@ COPY_BYTES = 1 << 30  # check copy: 1 GiB read + 1 GiB written
 
 
 def attn_kernel_name():
-    return {"persistent": "k_attn_pp", "wide": "k_attn_wide", "pipe": "k_attn_wide"}.get(
+    return {"persistent": "k_attn_pp", "wide": "k_attn_wide", "pipe": "k_attn_wide",
+            "duo": "k_attn_duo"}.get(
         os.environ.get("FLASHPREFILL_ATTN", ""), "k_attn")
 
 

@@ -120,6 +120,7 @@ int attn_impl() {
   if (e && strcmp(e, "persistent") == 0) return 2;
   if (e && strcmp(e, "wide") == 0) return 3;
   if (e && strcmp(e, "pipe") == 0) return 4;
+  if (e && strcmp(e, "duo") == 0) return 5;
   return 1;
 }
 
@@ -274,6 +275,9 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   } else if (impl == 4) {
     e = fp::launch_attn_pipe(a, p->dtype, p->head_dim,
                              static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap, s);
+  } else if (impl == 5) {
+    e = fp::launch_attn_duo(a, p->dtype, p->head_dim,
+                            static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap, s);
   } else {
     int cus = 0;
     e = device_cus(&cus);

@@ -71,6 +71,8 @@ hipError_t launch_attn_wide(const AttnArgs& a, int dtype, int head_dim, int64_t 
                             hipStream_t s);
 hipError_t launch_attn_pipe(const AttnArgs& a, int dtype, int head_dim, int64_t grid,
                             hipStream_t s);
+hipError_t launch_attn_duo(const AttnArgs& a, int dtype, int head_dim, int64_t grid,
+                            hipStream_t s);
 hipError_t launch_attn_pp(const AttnArgs& a, int dtype, int head_dim, int num_wg, hipStream_t s);
 
 }  // namespace fp

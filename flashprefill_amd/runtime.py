@@ -21,10 +21,11 @@ BLOCK = 128
 def attn_key_tile() -> int:
     """Keys per online-softmax step of the attention kernel the library runs:
     128 for the one-workgroup-per-row kernel (default), 64 for the persistent
-    kernel (FLASHPREFILL_ATTN=persistent) and the 64-queries-per-wave kernel
-    (FLASHPREFILL_ATTN=wide)."""
+    kernel (FLASHPREFILL_ATTN=persistent), the 64-key-step kernels
+    (FLASHPREFILL_ATTN=wide / pipe) and the two-group kernel, whose groups take
+    the two 64-key halves of each block (FLASHPREFILL_ATTN=duo)."""
     import os
-    return 64 if os.environ.get("FLASHPREFILL_ATTN") in ("persistent", "wide", "pipe") else 128
+    return 64 if os.environ.get("FLASHPREFILL_ATTN") in ("persistent", "wide", "pipe", "duo") else 128
 
 
 def _dtype_code(t: torch.Tensor) -> int:

@@ -80,7 +80,7 @@ def test_all_blocks_selected_is_dense_causal():
     _close(o, ref.permute(1, 0, 2))
 
 
-@pytest.mark.parametrize("kernel", ["rows", "persistent", "wide", "pipe"])
+@pytest.mark.parametrize("kernel", ["rows", "persistent", "wide", "pipe", "duo"])
 def test_all_blocks_selected_long_rows(kernel, monkeypatch):
     # 8300 tokens: 65 blocks per row (the wide kernel reloads its 64-entry
     # block-list chunk), a partial last block of 108 rows (its second half tile
@@ -99,7 +99,7 @@ def test_all_blocks_selected_long_rows(kernel, monkeypatch):
     _close(o, ref.permute(1, 0, 2).cpu())
 
 
-@pytest.mark.parametrize("kernel", ["rows", "persistent", "wide", "pipe"])
+@pytest.mark.parametrize("kernel", ["rows", "persistent", "wide", "pipe", "duo"])
 def test_growing_logits_rescale_every_block(kernel, monkeypatch):
     # every key block's logits exceed the previous block's by ~9 log2 units
     # (more than the kernels' rescaling slack of 8), so the running max moves

@@ -31,7 +31,7 @@ def case():
     return q, k, v, cu, ref
 
 
-@pytest.mark.parametrize("kernel", ["rows", "persistent", "wide", "pipe"])
+@pytest.mark.parametrize("kernel", ["rows", "persistent", "wide", "pipe", "duo"])
 def test_128k_sampled_rows_match_oracle_and_runs_are_identical(case, kernel, monkeypatch):
     monkeypatch.setenv("FLASHPREFILL_ATTN", kernel)
     q, k, v, cu, ref = case

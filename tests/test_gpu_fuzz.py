@@ -19,7 +19,7 @@ import torch
 from tests._parity import OUT_MAX_ABS, OUT_MEAN_ABS, run_stages
 
 pytestmark = pytest.mark.gpu
-KERNELS = ["rows", "persistent", "wide", "pipe"]
+KERNELS = ["rows", "persistent", "wide", "pipe", "duo"]
 
 
 def _case(seed):

@@ -22,7 +22,7 @@ pytestmark = pytest.mark.gpu
 
 # the attention kernels: one workgroup per row (default), the persistent one and
 # the 64-queries-per-wave one
-KERNELS = ["rows", "persistent", "wide", "pipe"]
+KERNELS = ["rows", "persistent", "wide", "pipe", "duo"]
 
 
 @pytest.fixture(params=KERNELS)
