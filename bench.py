@@ -564,6 +564,17 @@ def main():
             ent["traffic"] = int(stage_traffic[kk])
             ent["traffic_GBps"] = round(stage_traffic[kk] / (stage_ms[kk] * 1e-3) / 1e9, 1)
         search_roofline["kernels"][kk] = ent
+    # the fused search is compute-bound rather than HBM-bound: its score MFMAs
+    # (every causal (q-block, k-block) pair, 128 rows x d each) against the
+    # bf16 MFMA peak, and its exp2 rate (128 per pair below the diagonal, 1 on it)
+    pairs = Hq * nb * (nb + 1) // 2
+    score_flops = 2 * 128 * d * pairs
+    n_exp2 = Hq * (128 * nb * (nb - 1) // 2 + nb)
+    score_tf = score_flops / (stage_ms["k_search"] * 1e-3) / 1e12
+    search_roofline["kernels"]["k_search"]["compute"] = {
+        "score_mfma_flops": int(score_flops), "score_mfma_tflops": round(score_tf, 1),
+        "frac_of_bf16_mfma_peak": round(score_tf / PEAK_BF16_TFLOPS, 4),
+        "exp2": int(n_exp2), "exp2_per_ns": round(n_exp2 / (stage_ms["k_search"] * 1e6), 1)}
 
     traffic, traffic_src = None, None
     tf = traffic_file(S)
