@@ -134,6 +134,10 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
   const int g16 = lane >> 4, i16 = lane & 15;
   const int tr_row = 4 * (g16 >> 1) + (i16 >> 2);
   const int tr_col = 16 * (g16 & 1) + 4 * (i16 & 3);
+  // raised wave priority while this wave issues its P.V MFMAs: when both
+  // waves of a SIMD are ready, the MFMA stream goes first (measured 1-2 %
+  // faster; the same around S, or around the softmax instead, was not)
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const int t4 = u >> 1, hh = u & 1;
@@ -153,6 +157,7 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
       st.o[dt] = T::mfma32(as_vec8<T>(va), pb, st.o[dt]);
     }
   }
+  __builtin_amdgcn_s_setprio(0);
   if (jn >= 0) {
     // one barrier for two conditions: every wave is done with the V buffer,
     // and every wave's part of the next block's K (the only load in flight)
