@@ -64,3 +64,24 @@ def flash_prefill(
     call.run()
     if not direct:
         out.copy_(o2.view(B, S, Hq, d))
+
+
+class FlashPrefill(torch.autograd.Function):
+    """Class-level entry of the reference, which ``flash_prefill`` wraps
+    (``ops/flashprefill_native_forward.py:405-476``, called at :496-499):
+    ``FlashPrefill.apply(q, k, v, out, block_size, k_stride, attention_sink,
+    window, alpha, last_n_blocks_full, n_uniform, min_buget, topk)``.
+
+    Forward only; writes ``out`` in place and returns None, as there.
+    ``k_stride`` must equal ``block_size`` (:415; ValueError here, an assert
+    there); ``n_uniform`` and ``topk`` are accepted and unused, as there;
+    ``min_buget`` keeps the reference's spelling and is ``flash_prefill``'s
+    ``min_budget``."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, out, block_size=128, k_stride=128, attention_sink=2, window=4,
+                alpha=0.7, last_n_blocks_full=2, n_uniform=0, min_buget=0, topk=0):
+        if block_size != k_stride:
+            raise ValueError(f"block_size ({block_size}) must equal k_stride ({k_stride})")
+        flash_prefill(q, k, v, out, block_size, attention_sink, window, alpha,
+                      last_n_blocks_full, min_buget)

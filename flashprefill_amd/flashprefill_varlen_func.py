@@ -58,3 +58,22 @@ def flash_prefill_varlen_func(
     call.run()
     if o is not target:
         target.copy_(o)
+
+
+class FlashPrefill_varlen(torch.autograd.Function):
+    """Class-level entry of the reference, which ``flash_prefill_varlen_func``
+    wraps (``ops/flashprefill_varlen_func.py:577-720``, called at :739-743):
+    ``FlashPrefill_varlen.apply(q, k, v, o, cu_seqlens, max_seq_len,
+    block_size, k_stride, attention_sink, window, alpha, last_n_blocks)``.
+
+    Forward only; writes ``o`` in place and returns None, as there.
+    ``k_stride`` must equal ``block_size`` (:590; ValueError here, an assert
+    there)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, o, cu_seqlens, max_seq_len, block_size=128, k_stride=128,
+                attention_sink=2, window=4, alpha=0.7, last_n_blocks=2):
+        if block_size != k_stride:
+            raise ValueError(f"block_size ({block_size}) must equal k_stride ({k_stride})")
+        flash_prefill_varlen_func(q, k, v, o, cu_seqlens, max_seq_len, alpha, block_size,
+                                  attention_sink, window, last_n_blocks)

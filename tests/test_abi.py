@@ -131,3 +131,27 @@ def test_ops_shim_exposes_the_reference_module_layout():
     assert list(inspect.signature(flash_prefill_varlen_func).parameters)[:11] == [
         "q", "k", "v", "o", "cu_seqlens", "max_seq_len", "alpha", "block_size",
         "attention_sink", "window_size", "last_n_block"]
+
+
+def test_class_level_forwards_map_arguments_like_the_reference(monkeypatch):
+    # FlashPrefill.apply / FlashPrefill_varlen.apply (the reference's
+    # autograd.Function entry points) hand their arguments to the function
+    # entry points exactly as the reference's wrappers do, and check k_stride
+    import torch
+    import flashprefill_amd.flashprefill_native_forward as nf
+    import flashprefill_amd.flashprefill_varlen_func as vf
+    from ops.flashprefill_native_forward import FlashPrefill
+    from ops.flashprefill_varlen_func import FlashPrefill_varlen
+    seen = {}
+    monkeypatch.setattr(nf, "flash_prefill", lambda *a: seen.setdefault("native", a))
+    monkeypatch.setattr(vf, "flash_prefill_varlen_func", lambda *a: seen.setdefault("varlen", a))
+    q, k, v, o = (torch.zeros(1) for _ in range(4))
+    assert FlashPrefill.apply(q, k, v, o, 128, 128, 3, 5, 0.25, 1, 7, 11, 13) is None
+    assert seen["native"][4:] == (128, 3, 5, 0.25, 1, 11)
+    cu = torch.zeros(2, dtype=torch.int32)
+    assert FlashPrefill_varlen.apply(q, k, v, o, cu, 4096, 128, 128, 3, 5, 0.25, 1) is None
+    assert seen["varlen"][5:] == (4096, 0.25, 128, 3, 5, 1)
+    with pytest.raises(ValueError):
+        FlashPrefill.apply(q, k, v, o, 128, 64)
+    with pytest.raises(ValueError):
+        FlashPrefill_varlen.apply(q, k, v, o, cu, 4096, 128, 64)

@@ -51,6 +51,31 @@ def test_native_batched_api_matches_oracle():
     _close(out, ref)
 
 
+def test_class_level_entry_points_match_the_functions():
+    # FlashPrefill_varlen.apply / FlashPrefill.apply (the reference's
+    # autograd.Function entry points) give the function entry points' output
+    # bit for bit
+    from ops.flashprefill_native_forward import FlashPrefill
+    from ops.flashprefill_varlen_func import FlashPrefill_varlen
+    lens = [700, 300]
+    T = sum(lens)
+    q, k, v = _rand((T, 8, 128), 21, scale=1.5), _rand((T, 2, 128), 22, scale=1.5), _rand((T, 2, 128), 23)
+    cu = torch.tensor([0, 700, T], dtype=torch.int32, device=DEV)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    o1, o2 = torch.empty_like(qd), torch.empty_like(qd)
+    flash_prefill_varlen_func(qd, kd, vd, o1, cu, 700, 0.12, 128, 2, 4, 2)
+    assert FlashPrefill_varlen.apply(qd, kd, vd, o2, cu, 700, 128, 128, 2, 4, 0.12, 2) is None
+    B, S = 2, 500
+    qb, kb, vb = (x.to(DEV) for x in (_rand((B, S, 8, 128), 24, scale=1.5),
+                                      _rand((B, S, 2, 128), 25, scale=1.5), _rand((B, S, 2, 128), 26)))
+    o3, o4 = torch.empty_like(qb), torch.empty_like(qb)
+    flash_prefill(qb, kb, vb, o3, 128, 2, 4, 0.7, 2, 3)
+    assert FlashPrefill.apply(qb, kb, vb, o4, 128, 128, 2, 4, 0.7, 2, 0, 3, 0) is None
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    assert torch.equal(o3, o4)
+
+
 def test_strided_inputs_match_contiguous():
     # q/k/v carved out of one fused qkv projection output, as vLLM does
     T, Hq, Hkv, d = 900, 8, 2, 128
