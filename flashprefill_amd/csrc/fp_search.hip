@@ -285,34 +285,30 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
 
       // acc[rg][v] = Q[32 rg + 8 (v/4) + 4 half + v%4] . mk[j]
       float mx = -INFINITY, sum = 0.0f, m;
+#pragma unroll
+      for (int rg = 0; rg < 4; ++rg)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc[rg][v]);
       if (tile + 1 < ntiles) {  // every column j < i: all 128 rows count
-#pragma unroll
-        for (int rg = 0; rg < 4; ++rg)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc[rg][v]);
         m = pair32_max(mx) * c;
 #pragma unroll
         for (int rg = 0; rg < 4; ++rg)
 #pragma unroll
           for (int v = 0; v < 16; ++v) sum += __builtin_amdgcn_exp2f(fmaf(acc[rg][v], c, -m));
-      } else {  // last tile: j < i all rows, j == i row 127 only, j > i none
-        const bool full = j < i, diag = j == i;
-#pragma unroll
-        for (int rg = 0; rg < 4; ++rg)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int row = 32 * rg + 8 * (v >> 2) + 4 * half + (v & 3);
-            if (full || (diag && row == kBlock - 1)) mx = fmaxf(mx, acc[rg][v]);
-          }
+      } else {
+        // last tile: j < i all rows, j == i row 127 only (acc[3][15] of the
+        // upper half-wave), j > i none. The case is uniform over a lane's 64
+        // values, so the full-tile reduction runs for every lane and one
+        // select per lane picks the result (the same arithmetic on the rows
+        // that count, no per-element masking)
+        const bool full = j < i, row127 = j == i && half == 1;
+        mx = full ? mx : (row127 ? acc[3][15] : -INFINITY);
         m = pair32_max(mx) * c;
 #pragma unroll
         for (int rg = 0; rg < 4; ++rg)
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int row = 32 * rg + 8 * (v >> 2) + 4 * half + (v & 3);
-            if (full || (diag && row == kBlock - 1))
-              sum += __builtin_amdgcn_exp2f(fmaf(acc[rg][v], c, -m));
-          }
+          for (int v = 0; v < 16; ++v) sum += __builtin_amdgcn_exp2f(fmaf(acc[rg][v], c, -m));
+        sum = full ? sum : (row127 ? __builtin_amdgcn_exp2f(fmaf(acc[3][15], c, -m)) : 0.0f);
       }
       sum = pair32_sum(sum);
       if (half == 0 && jv) {
