@@ -177,18 +177,17 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
 
   int item, h;
   map_item(blockIdx.x, a.Hq, item, h);
-  const int64_t nitems = a.tab.seq_tile[a.B];
+  // the item record (one scalar load) carries everything the row needs, so
+  // its count and first tile loads follow after one scalar-load latency
+  const int64_t nitems = sld(a.tab.seq_tile + a.B);
   if (item >= nitems) return;
-  const int b = a.tab.items[item].b;
-  const int i = a.tab.items[item].i;
-  const int64_t tile_b = a.tab.seq_tile[b];
-  const int L = a.tab.seq_len[b];
-  const int64_t t0 = a.tab.seq_start[b];
-  const int64_t row_tri = static_cast<int64_t>(h) * a.tri_cap + a.tab.seq_tri[b] +
-                          static_cast<int64_t>(i) * (i + 1) / 2;
+  const ItemRec rec = sld(a.tab.items + item);
+  const int i = rec.i, L = rec.L;
+  const int64_t t0 = rec.t0;
+  const int64_t row_tri = static_cast<int64_t>(h) * a.tri_cap + rec.tri;
   // counts and lists come from the search stage; clamp them to the row's
   // capacity so a stale workspace can never index outside the sequence
-  const int ncnt = min(max(a.cnt[static_cast<int64_t>(h) * a.nb_sum_cap + tile_b + i], 0), i + 1);
+  const int ncnt = min(max(sld(a.cnt + static_cast<int64_t>(h) * a.nb_sum_cap + rec.tile), 0), i + 1);
   const int32_t* list = a.idx + row_tri;
   const int kvh = h / (a.Hq / a.Hkv);
 

@@ -206,17 +206,16 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
   float* ml = pl + a.nb_max;
   int item, h;
   map_item(blockIdx.x, a.Hq, item, h);
-  const int64_t nitems = a.tab.seq_tile[a.B];
+  // the item record (one scalar load) carries everything the query-block
+  // loads need, so they are issued one scalar-load latency after the start
+  const int64_t nitems = sld(a.tab.seq_tile + a.B);
   if (item >= nitems) return;
-  const int b = a.tab.items[item].b;
-  const int i = a.tab.items[item].i;
-  const int64_t tile_b = a.tab.seq_tile[b];
-  const int nb = static_cast<int>(a.tab.seq_tile[b + 1] - tile_b);
-  const int L = a.tab.seq_len[b];
-  const int64_t t0 = a.tab.seq_start[b];
+  const ItemRec rec = sld(a.tab.items + item);
+  const int b = rec.b, i = rec.i, L = rec.L;
+  const int64_t tile_b = rec.tile - i;
+  const int64_t t0 = rec.t0;
   const int n = i + 1;
-  const int64_t row_tri = static_cast<int64_t>(h) * a.tri_cap + a.tab.seq_tri[b] +
-                          static_cast<int64_t>(i) * (i + 1) / 2;
+  const int64_t row_tri = static_cast<int64_t>(h) * a.tri_cap + rec.tri;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
 
   if constexpr (FROM_SCORES) {
@@ -323,7 +322,8 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
   }
   __syncthreads();
   int32_t* list = a.idx + row_tri;
-  int32_t* count = a.cnt + static_cast<int64_t>(h) * a.nb_sum_cap + tile_b + i;
+  int32_t* count = a.cnt + static_cast<int64_t>(h) * a.nb_sum_cap + rec.tile;
+  const int nb = static_cast<int>(sld(a.tab.seq_tile + b + 1) - tile_b);
   select_row(pl, ml, n, i, nb, a, list, count, dyn4);
 }
 
