@@ -321,25 +321,32 @@ def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines):
     print("bench: timing", file=sys.stderr, flush=True)
     ms_total = timed(call.run, steps)
 
+    # t_search is pool + score + select, the search of the reference's path
+    # (its block-table setup is orchestration); the plan kernel, which builds
+    # the work tables of both the search and the attention, is timed apart
+    # and reported beside it
     def search_stage():
-        call.plan()
         call.pool()
         call.search()
 
+    ms_plan = timed(call.plan, max(3, steps))
     ms_search = timed(search_stage, max(3, steps))
-    # the same split inside full calls: events between the search stages and
-    # the attention of each staged call (same kernels as call.run())
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(max(3, steps))]
+    # the same split inside full calls: events around the plan, the search
+    # stages and the attention of each staged call (same kernels as call.run())
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(max(3, steps))]
     torch.cuda.synchronize()
-    for e3 in ev:
-        e3[0].record()
+    for e4 in ev:
+        e4[0].record()
+        call.plan()
+        e4[1].record()
         search_stage()
-        e3[1].record()
+        e4[2].record()
         call.attn()
-        e3[2].record()
+        e4[3].record()
     torch.cuda.synchronize()
-    in_call_search = sum(e3[0].elapsed_time(e3[1]) for e3 in ev) / len(ev)
-    in_call_total = sum(e3[0].elapsed_time(e3[2]) for e3 in ev) / len(ev)
+    in_call_plan = sum(e4[0].elapsed_time(e4[1]) for e4 in ev) / len(ev)
+    in_call_search = sum(e4[1].elapsed_time(e4[2]) for e4 in ev) / len(ev)
+    in_call_total = sum(e4[0].elapsed_time(e4[3]) for e4 in ev) / len(ev)
     ms_pool = timed(call.pool, max(3, steps))
     ms_score = timed(call.search, max(3, steps))
     ms_attn = timed(call.attn, max(3, steps))
@@ -351,10 +358,13 @@ def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines):
     dense_flops = sum(dense_causal_flops(s, Hq, d) for s in seq_lens)
     out = {
         "ms_total": ms_total, "ms_search": ms_search, "ms_attn": ms_attn,
-        "ms_pool": ms_pool, "ms_score": ms_score,
-        "search_share": ms_search / ms_total, "executed_blocks": n_exec,
-        "in_call_split": {"ms_search": in_call_search, "ms_total": in_call_total,
-                          "search_share": in_call_search / in_call_total},
+        "ms_pool": ms_pool, "ms_score": ms_score, "ms_plan": ms_plan,
+        "search_share": ms_search / ms_total,
+        "search_share_incl_plan": (ms_search + ms_plan) / ms_total, "executed_blocks": n_exec,
+        "in_call_split": {"ms_plan": in_call_plan, "ms_search": in_call_search,
+                          "ms_total": in_call_total,
+                          "search_share": in_call_search / in_call_total,
+                          "search_share_incl_plan": (in_call_plan + in_call_search) / in_call_total},
         "density": n_exec / causal_blocks, "executed_tflops": exec_tflops,
         "mfma_frac": exec_tflops / PEAK_BF16_TFLOPS,
         "effective_tflops": dense_flops / (ms_total * 1e-3) / 1e12,
@@ -604,10 +614,15 @@ def main():
                                "Llama-3-8B heads", "seq_len": S, "num_q_heads": Hq,
                    "num_kv_heads": Hkv, "head_dim": d, "block_size": 128, "alpha": args.alpha,
                    "attention_sink": 2, "window_size": 4, "last_n_block": 2, "seed": args.seed},
+        # t_search = pool + score + select; the plan kernel (work tables of
+        # both stages) is t_plan, and the shares including it are reported too
         "t_search_ms": round(ms_search, 4),
+        "t_plan_ms": round(r["ms_plan"], 4),
         "t_attn_ms": round(ms_attn, 4),
         "search_share": round(ms_search / ms_total, 4),
         "search_share_in_call": round(r["in_call_split"]["search_share"], 4),
+        "search_share_incl_plan": round(r["search_share_incl_plan"], 4),
+        "search_share_incl_plan_in_call": round(r["in_call_split"]["search_share_incl_plan"], 4),
         "density": round(density, 5),
         "executed_blocks": n_exec,
         "executed_tflops": round(exec_tflops, 2),
