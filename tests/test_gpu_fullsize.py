@@ -1,5 +1,5 @@
 """Parity at the full config-3 size (131072 tokens, 32 q / 8 kv heads,
-d = 128, bf16): the whole operator runs on the GPU through the C ABI, and a
+d = 128, bf16; and one 262144-token sequence for the default kernel): the whole operator runs on the GPU through the C ABI, and a
 sample of (head, q-block) rows from light to heavy is recomputed by the
 oracle's row pipeline (pooled K of all blocks, scores, normalisation,
 selection, attention). The selection lists must agree (threshold flips are
@@ -31,10 +31,7 @@ def case():
     return q, k, v, cu, ref
 
 
-@pytest.mark.parametrize("kernel", ["rows", "persistent", "wide", "pipe", "duo"])
-def test_128k_sampled_rows_match_oracle_and_runs_are_identical(case, kernel, monkeypatch):
-    monkeypatch.setenv("FLASHPREFILL_ATTN", kernel)
-    q, k, v, cu, ref = case
+def _check_sampled_rows(S, q, k, v, cu, ref, label):
     outs = []
     for _ in range(2):
         o = torch.full_like(q, float("nan"))
@@ -69,6 +66,28 @@ def test_128k_sampled_rows_match_oracle_and_runs_are_identical(case, kernel, mon
         assert d.max().item() <= OUT_MAX_ABS
         assert d.mean().item() <= OUT_MEAN_ABS
         checked += 1
-    print(f"  {kernel}: threshold flips {flips}, rows checked {checked}/{len(ref)}", flush=True)
+    print(f"  {label}: threshold flips {flips}, rows checked {checked}/{len(ref)}", flush=True)
     assert flips <= 1
     assert checked >= len(ref) - 1
+
+
+@pytest.mark.parametrize("kernel", ["rows", "persistent", "wide", "pipe", "duo"])
+def test_128k_sampled_rows_match_oracle_and_runs_are_identical(case, kernel, monkeypatch):
+    monkeypatch.setenv("FLASHPREFILL_ATTN", kernel)
+    q, k, v, cu, ref = case
+    _check_sampled_rows(S, q, k, v, cu, ref, kernel)
+
+
+S256 = 262144
+ROWS256 = [(0, 2047), (17, 1800), (4, 1024), (29, 300), (11, 5), (22, 0)]
+
+
+def test_256k_sampled_rows_match_oracle_and_runs_are_identical(monkeypatch):
+    # 2048 blocks per row: the search's p / m arrays take 16 KB of LDS (three
+    # workgroups per CU instead of four) and the lists are twice as long
+    monkeypatch.delenv("FLASHPREFILL_ATTN", raising=False)
+    spec = synth.llama_spec(S256, seed=256)
+    q, k, v, cu = synth.make_inputs(spec, device="cuda:0")
+    ref = O.flashprefill_rows(q.cpu(), k.cpu(), v.cpu(), ROWS256, alpha=ALPHA, attention_sink=2,
+                              window=4, last_n=2, native=False)
+    _check_sampled_rows(S256, q, k, v, cu, ref, "rows at 256K")
