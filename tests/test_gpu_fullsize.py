@@ -91,3 +91,50 @@ def test_256k_sampled_rows_match_oracle_and_runs_are_identical(monkeypatch):
     ref = O.flashprefill_rows(q.cpu(), k.cpu(), v.cpu(), ROWS256, alpha=ALPHA, attention_sink=2,
                               window=4, last_n=2, native=False)
     _check_sampled_rows(S256, q, k, v, cu, ref, "rows at 256K")
+
+
+# config 4 at full size: Qwen2.5 shapes (28 q / 4 kv heads), ragged batch
+# {256K, 64K, 17K, 3K, 1K}, alpha 0.08; (sequence, head, q-block) samples
+ROWS_VARLEN = {0: [(3, 2047), (27, 900), (10, 1)], 1: [(14, 511), (0, 40)],
+               2: [(20, 135), (7, 3)], 3: [(25, 23)], 4: [(1, 7), (18, 0)]}
+
+
+def test_config4_ragged_batch_sampled_rows_match_oracle(monkeypatch):
+    monkeypatch.delenv("FLASHPREFILL_ATTN", raising=False)
+    spec = synth.qwen_varlen_spec()
+    q, k, v, cu = synth.make_inputs(spec, device="cuda:0")
+    o = torch.full_like(q, float("nan"))
+    call = FlashPrefillCall(q, k, v, o, cu, max(spec.seq_lens), alpha=0.08, attention_sink=2,
+                            window_size=4, last_n_block=2)
+    call.run()
+    torch.cuda.synchronize()
+    assert call.status() == 0
+    assert not torch.isnan(o).any(), "unwritten output rows"
+    tile, tri, start, _ = call.seq_tables()
+    cnt = call.counts().cpu()
+    idx = call.index_lists().cpu()
+    flips, checked, total = 0, 0, 0
+    for b, rows in ROWS_VARLEN.items():
+        t0, S = start[b], spec.seq_lens[b]
+        ref = O.flashprefill_rows(q[t0:t0 + S].cpu(), k[t0:t0 + S].cpu(), v[t0:t0 + S].cpu(), rows,
+                                  alpha=0.08, attention_sink=2, window=4, last_n=2, native=False)
+        nb = (S + 127) // 128
+        for (h, i), (sel_o, out_o) in ref.items():
+            total += 1
+            c = int(cnt[h, tile[b] + i])
+            base = tri[b] + i * (i + 1) // 2
+            lst = idx[h, base:base + c]
+            assert bool((lst[1:] > lst[:-1]).all()), f"row {(b, h, i)} list not ascending"
+            gsel = torch.zeros(nb, dtype=torch.bool)
+            gsel[lst.long()] = True
+            row_flips = int((gsel != sel_o).sum())
+            flips += row_flips
+            if row_flips:
+                continue
+            d = (o[t0 + i * 128:t0 + min((i + 1) * 128, S), h].float().cpu() - out_o.float()).abs()
+            assert d.max().item() <= OUT_MAX_ABS
+            assert d.mean().item() <= OUT_MEAN_ABS
+            checked += 1
+    print(f"  config 4: threshold flips {flips}, rows checked {checked}/{total}", flush=True)
+    assert flips <= 1
+    assert checked >= total - 1
