@@ -68,19 +68,12 @@ __device__ __forceinline__ void st16(void* p, uint4 v) { *reinterpret_cast<uint4
 // ---------------------------------------------------------------------------
 // wave / block reductions (wave64)
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float xor32_f(float x) { return __shfl_xor(x, 32); }
-
 __device__ __forceinline__ float wave_max(float x) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
   return x;
 }
 __device__ __forceinline__ double wave_sum_d(double x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
-  return x;
-}
-__device__ __forceinline__ int64_t wave_sum_i64(int64_t x) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
   return x;
@@ -94,18 +87,6 @@ __device__ __forceinline__ float block_max(float x, float* red) {
   __syncthreads();
   float r = red[0];
   for (int k = 1; k < nw; ++k) r = fmaxf(r, red[k]);
-  __syncthreads();
-  return r;
-}
-
-// Block-wide fp64 sum; `red` needs blockDim.x/64 doubles.
-__device__ __forceinline__ double block_sum_d(double x, double* red) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  x = wave_sum_d(x);
-  if (lane == 0) red[w] = x;
-  __syncthreads();
-  double r = 0.0;
-  for (int k = 0; k < nw; ++k) r += red[k];
   __syncthreads();
   return r;
 }
