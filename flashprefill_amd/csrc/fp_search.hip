@@ -269,7 +269,6 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
     for (int tile = w; tile < ntiles; tile += 4) {
       const int j = 32 * tile + l32;
       const bool jv = j < n;
-      if (tile != w) load_kb(tile);
       f32x16 acc[4];
 #pragma unroll
       for (int rg = 0; rg < 4; ++rg) acc[rg] = f32x16{};
@@ -282,6 +281,13 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
           acc[rg] = T::mfma32(as_vec8<T>(qop), kb[s], acc[rg]);
         }
 
+      // the wave's next key tile, loaded as one burst into kb (dead once the
+      // MFMAs above have read it) so that its latency passes behind this
+      // tile's max / exp2 / sum; loads issued between the MFMAs instead
+      // stalled the MFMA stream and measured slower
+      __builtin_amdgcn_sched_barrier(0);
+      if (tile + 4 < ntiles) load_kb(tile + 4);
+      __builtin_amdgcn_sched_barrier(0);
       // acc[rg][v] = Q[32 rg + 8 (v/4) + 4 half + v%4] . mk[j]
       float mx = -INFINITY, sum = 0.0f, m;
 #pragma unroll
