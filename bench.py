@@ -76,15 +76,15 @@ def timed(fn, reps, stream=None):
 COPY_BYTES = 1 << 30  # check copy: 1 GiB read + 1 GiB written
 
 
+ATTN_KERNEL = "k_attn"
+
+
 def attn_kernel_name():
-    return {"persistent": "k_attn_pp", "wide": "k_attn_wide", "pipe": "k_attn_wide",
-            "duo": "k_attn_duo"}.get(
-        os.environ.get("FLASHPREFILL_ATTN", ""), "k_attn")
+    return ATTN_KERNEL
 
 
 def traffic_file(S):
-    tag = "k_attn_pipe" if os.environ.get("FLASHPREFILL_ATTN") == "pipe" else attn_kernel_name()
-    return os.path.join(ROOT, "profiles", f"attn_traffic_llama{S // 1024}k_{tag}.json")
+    return os.path.join(ROOT, "profiles", f"attn_traffic_llama{S // 1024}k_{ATTN_KERNEL}.json")
 
 
 def stage_traffic_file(S):

@@ -24,7 +24,7 @@ FP_DTYPE_BF16 = 0
 FP_DTYPE_F16 = 1
 FP_STATUS_SEQ_TOO_LONG = 1
 FP_STATUS_BAD_CU_SEQLENS = 2
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 EXPORTS = (
     "fp_workspace_layout", "fp_workspace_bytes", "fp_flashprefill", "fp_plan", "fp_pool_k",
@@ -59,7 +59,7 @@ class FpWsLayout(ctypes.Structure):
         ("total_bytes", ctypes.c_size_t), ("status_off", ctypes.c_size_t),
         ("seq_tile_off", ctypes.c_size_t), ("seq_tri_off", ctypes.c_size_t),
         ("seq_start_off", ctypes.c_size_t), ("seq_len_off", ctypes.c_size_t),
-        ("items_off", ctypes.c_size_t), ("sched_off", ctypes.c_size_t),
+        ("items_off", ctypes.c_size_t),
         ("mk_off", ctypes.c_size_t),
         ("cnt_off", ctypes.c_size_t), ("idx_off", ctypes.c_size_t),
         ("nb_sum_cap", ctypes.c_int64), ("tri_cap", ctypes.c_int64),

@@ -110,11 +110,6 @@ __device__ __forceinline__ uint64_t scalar_addr(const void* p) {
       static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(b >> 32)));
   return (static_cast<uint64_t>(hi) << 32) | lo;
 }
-// one load: scalar base + 32-bit lane offset
-__device__ __forceinline__ void dma16_saddr(void* lds_slice, const void* base, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, %2"
-               :: "s"(lds_addr(lds_slice)), "v"(voff), "s"(scalar_addr(base)) : "memory", "m0");
-}
 // one load: per-lane 64-bit address
 __device__ __forceinline__ void dma16_vaddr(void* lds_slice, const void* src) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, off"
@@ -126,12 +121,6 @@ __device__ __forceinline__ void dma16_sbase_m0(uint32_t lds, uint64_t sbase, uin
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 1\n\tglobal_load_lds_dwordx4 %1, %2"
                :: "s"(lds), "v"(voff), "s"(sbase) : "memory", "m0");
 }
-// one load: per-lane 64-bit address, LDS slice as a wave-uniform LDS byte address
-__device__ __forceinline__ void dma16_vaddr_at(uint32_t lds, const void* src) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tglobal_load_lds_dwordx4 %1, off"
-               :: "s"(lds), "v"(src) : "memory", "m0");
-}
-
 // Direct-to-LDS loads of one 128 x D tile (block j of a K or V head). Wave w
 // fills the 1 KB LDS slices w*NI .. w*NI+NI-1; in each slice lane l writes
 // physical chunk l % CH of row slice*RPW + l / CH, so it fetches logical
@@ -185,29 +174,6 @@ __device__ __forceinline__ void issue_tile(uint4* lds, const uint16_t* base, int
     }
   }
 }
-
-// Lane offsets and direct-to-LDS loads of a half tile (64 rows of a 128-row
-// block; 16 KB at d = 128): wave w fills 1 KB slices w*NI .. w*NI+NI-1.
-// off[q] is this lane's byte offset from the half tile's first row for
-// slice w*NI + q, so every load of a tile uses one scalar base address
-// (64 * stride * 2 < 2^31 is checked on the host).
-template <int D>
-struct HalfLanes {
-  static constexpr int CH = D / 8;
-  static constexpr int RPW = 64 / CH;             // rows per 1 KB slice
-  static constexpr int NI = CH / 4;               // slices per wave per half tile
-  static constexpr int PER = D == 128 ? 4 : 2;    // period of swz over the slice index
-  uint32_t off[NI];
-  __device__ __forceinline__ void init(int64_t stride, int w, int lane) {
-#pragma unroll
-    for (int q = 0; q < NI; ++q) {
-      const int r = (w * NI + q) * RPW + lane / CH;
-      const int c = (lane % CH) ^ swz<D>(r);
-      off[q] = static_cast<uint32_t>((r * stride + 8 * c) * 2);
-    }
-  }
-};
-
 
 // Reductions over the two 32-lane halves of a wave (lane l with l ^ 32):
 // v_permlane32_swap exchanges the halves of its two operands, so max / sum

@@ -103,43 +103,11 @@ int layout(const fp_problem* p, fp_ws_layout* L) {
   L->seq_start_off = off;  off = align_up(off + 8 * B);
   L->seq_len_off = off;    off = align_up(off + 4 * B);
   L->items_off = off;      off = align_up(off + sizeof(fp::ItemRec) * cap);
-  L->sched_off = off;      off = align_up(off + 4 * 16);
   L->mk_off = off;         off = align_up(off + 2 * cap * Hkv * d);
   L->cnt_off = off;        off = align_up(off + 4 * Hq * cap);
   L->idx_off = off;        off = align_up(off + 4 * Hq * tri);
   L->total_bytes = off;
   return FP_OK;
-}
-
-// Attention kernel choice, read at every call: the one-workgroup-per-row
-// kernel (default), the persistent two-group kernel
-// (FLASHPREFILL_ATTN=persistent) or the two-wave, 64-queries-per-wave row
-// kernel (FLASHPREFILL_ATTN=wide).
-int attn_impl() {
-  const char* e = getenv("FLASHPREFILL_ATTN");
-  if (e && strcmp(e, "persistent") == 0) return 2;
-  if (e && strcmp(e, "wide") == 0) return 3;
-  if (e && strcmp(e, "pipe") == 0) return 4;
-  if (e && strcmp(e, "duo") == 0) return 5;
-  return 1;
-}
-
-// Workgroups of the persistent kernel: one per CU, a multiple of the 8 XCDs.
-hipError_t device_cus(int* out) {
-  static int cache[64] = {0};
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return e;
-  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-  if (cache[dev] == 0) {
-    int n = 0;
-    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e != hipSuccess) return e;
-    n = (n / 8) * 8;
-    cache[dev] = n < 8 ? 8 : n;
-  }
-  *out = cache[dev];
-  return hipSuccess;
 }
 
 fp::SeqTables tables(const fp_ws_layout& L, void* ws) {
@@ -179,7 +147,7 @@ int run_plan(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   a.max_seq_len = p->max_seq_len;
   a.nb_max = L.nb_max;
   a.total_tokens = p->total_tokens;
-  a.sched = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + L.sched_off);
+  a.nb_sum_cap = L.nb_sum_cap;
   const hipError_t e = fp::launch_plan(a, s);
   return e == hipSuccess ? FP_OK : hip_fail(e, "plan launch");
 }
@@ -263,26 +231,8 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   a.Hq = p->num_q_heads;
   a.Hkv = p->num_kv_heads;
   a.sm_scale_log2 = sm_scale_log2(p->head_dim);
-  a.sched = reinterpret_cast<int32_t*>(base + L.sched_off);
-  hipError_t e;
-  const int impl = attn_impl();
-  if (impl == 1) {
-    e = fp::launch_attn(a, p->dtype, p->head_dim,
-                        static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap, s);
-  } else if (impl == 3) {
-    e = fp::launch_attn_wide(a, p->dtype, p->head_dim,
-                             static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap, s);
-  } else if (impl == 4) {
-    e = fp::launch_attn_pipe(a, p->dtype, p->head_dim,
-                             static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap, s);
-  } else if (impl == 5) {
-    e = fp::launch_attn_duo(a, p->dtype, p->head_dim,
-                            static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap, s);
-  } else {
-    int cus = 0;
-    e = device_cus(&cus);
-    if (e == hipSuccess) e = fp::launch_attn_pp(a, p->dtype, p->head_dim, cus, s);
-  }
+  const hipError_t e = fp::launch_attn(a, p->dtype, p->head_dim,
+                                       static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap, s);
   return e == hipSuccess ? FP_OK : hip_fail(e, "attention launch");
 }
 
@@ -290,7 +240,7 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
 
 extern "C" {
 
-int fp_abi_version(void) { return 2; }
+int fp_abi_version(void) { return 3; }
 
 const char* fp_last_error(void) { return g_last_error.c_str(); }
 

@@ -9,13 +9,13 @@ namespace fp {
 
 struct PlanArgs {
   SeqTables tab;
-  int32_t* sched;     // attention work-queue counters (zeroed here)
   const int32_t* cu;  // nullable: uniform batch
   int32_t B;
   int32_t uniform_len;
   int32_t max_seq_len;
   int32_t nb_max;
   int64_t total_tokens;
+  int64_t nb_sum_cap;  // workspace capacity of sum_b NB_b (items, counts, pooled K)
 };
 
 struct PoolArgs {
@@ -57,7 +57,6 @@ struct AttnArgs {
   const int32_t* cnt;
   int64_t tri_cap;
   int64_t nb_sum_cap;
-  int32_t* sched;      // 8 per-XCD queue counters + 1 finish counter (persistent kernel)
   int32_t B, Hq, Hkv;
   float sm_scale_log2;
 };
@@ -67,12 +66,5 @@ hipError_t launch_pool(const PoolArgs& a, int dtype, int head_dim, int64_t grid,
 hipError_t launch_search(const SearchArgs& a, int dtype, int head_dim, int64_t grid,
                          bool from_scores, hipStream_t s);
 hipError_t launch_attn(const AttnArgs& a, int dtype, int head_dim, int64_t grid, hipStream_t s);
-hipError_t launch_attn_wide(const AttnArgs& a, int dtype, int head_dim, int64_t grid,
-                            hipStream_t s);
-hipError_t launch_attn_pipe(const AttnArgs& a, int dtype, int head_dim, int64_t grid,
-                            hipStream_t s);
-hipError_t launch_attn_duo(const AttnArgs& a, int dtype, int head_dim, int64_t grid,
-                            hipStream_t s);
-hipError_t launch_attn_pp(const AttnArgs& a, int dtype, int head_dim, int num_wg, hipStream_t s);
 
 }  // namespace fp

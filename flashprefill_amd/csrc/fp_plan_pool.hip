@@ -40,6 +40,33 @@ __device__ int64_t block_exscan_i64(int64_t v, int64_t* red, int64_t* total) {
   return wave_off + x - v;
 }
 
+// Block-wide inclusive running maximum of one int64 per thread.
+__device__ int64_t block_inscan_max_i64(int64_t v, int64_t* red, int64_t* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  int64_t x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t y = __shfl_up(x, o);
+    if (lane >= o) x = max(x, y);
+  }
+  if (lane == 63) red[w] = x;
+  __syncthreads();
+  if (w == 0) {
+    int64_t r = lane < nw ? red[lane] : INT64_MIN;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int64_t y = __shfl_up(r, o);
+      if (lane >= o) r = max(r, y);
+    }
+    if (lane < nw) red[lane] = r;
+  }
+  __syncthreads();
+  const int64_t res = w > 0 ? max(red[w - 1], x) : x;
+  *total = red[nw - 1];
+  __syncthreads();
+  return res;
+}
+
 __global__ __launch_bounds__(1024) void k_plan(PlanArgs a) {
   __shared__ int32_t s_pre[kMaxBatch + 1];  // NB prefix over sequences
   __shared__ int32_t s_lvl[kMaxBlocks];     // per q-block level: counts, then cursors
@@ -48,31 +75,59 @@ __global__ __launch_bounds__(1024) void k_plan(PlanArgs a) {
   const int t = threadIdx.x, nt = blockDim.x;
   const SeqTables& tab = a.tab;
   if (t == 0) s_status = 0u;
-  if (t < 16) a.sched[t] = 0;
   __syncthreads();
 
-  // 1. per-sequence lengths and validity
-  for (int b = t; b < a.B; b += nt) {
-    int64_t start, end;
-    if (a.cu) {
-      start = a.cu[b];
-      end = a.cu[b + 1];
-    } else {
-      start = static_cast<int64_t>(b) * a.uniform_len;
-      end = start + a.uniform_len;
+  // 1. per-sequence lengths and validity. A sequence is kept only if it lies
+  //    inside [0, total_tokens], is not longer than max_seq_len, and starts at
+  //    or after every earlier cu_seqlens entry (inclusive running maximum), so
+  //    the kept sequences are disjoint and ordered: their lengths add up to at
+  //    most total_tokens and sum_b NB_b stays within nb_sum_cap.
+  int64_t run_max = INT64_MIN;
+  int64_t nb_tot = 0;
+  for (int base = 0; base < a.B; base += nt) {
+    const int b = base + t;
+    int64_t start = 0, end = 0;
+    if (b < a.B) {
+      if (a.cu) {
+        start = a.cu[b];
+        end = a.cu[b + 1];
+      } else {
+        start = static_cast<int64_t>(b) * a.uniform_len;
+        end = start + a.uniform_len;
+      }
     }
-    int64_t len = end - start;
-    if (start < 0 || len < 0 || end > a.total_tokens) {
-      atomicOr(&s_status, FP_STATUS_BAD_CU_SEQLENS);
-      len = 0;
-      start = 0;
-    } else if (len > a.max_seq_len) {
-      atomicOr(&s_status, FP_STATUS_SEQ_TOO_LONG);
-      len = 0;
+    int64_t chunk_max;
+    const int64_t incl = max(run_max, block_inscan_max_i64(b < a.B ? start : INT64_MIN, s_red,
+                                                           &chunk_max));
+    run_max = max(run_max, chunk_max);
+    int64_t nb = 0;
+    if (b < a.B) {
+      int64_t len = end - start;
+      if (start < 0 || len < 0 || end > a.total_tokens || incl > start) {
+        atomicOr(&s_status, FP_STATUS_BAD_CU_SEQLENS);
+        len = 0;
+        start = 0;
+      } else if (len > a.max_seq_len) {
+        atomicOr(&s_status, FP_STATUS_SEQ_TOO_LONG);
+        len = 0;
+      }
+      tab.seq_start[b] = start;
+      tab.seq_len[b] = static_cast<int32_t>(len);
+      nb = (len + kBlock - 1) / kBlock;
+      s_pre[b] = static_cast<int32_t>(nb);
     }
-    tab.seq_start[b] = start;
-    tab.seq_len[b] = static_cast<int32_t>(len);
-    s_pre[b] = static_cast<int32_t>((len + kBlock - 1) / kBlock);
+    int64_t chunk_nb;
+    block_exscan_i64(nb, s_red, &chunk_nb);
+    nb_tot += chunk_nb;
+  }
+  // The rule above bounds sum NB by the workspace capacity; should a table
+  // ever exceed it, every sequence is skipped rather than written past it.
+  if (nb_tot > a.nb_sum_cap) {
+    for (int b = t; b < a.B; b += nt) {
+      tab.seq_len[b] = 0;
+      s_pre[b] = 0;
+    }
+    if (t == 0) s_status |= FP_STATUS_BAD_CU_SEQLENS;
   }
   for (int i = t; i < a.nb_max; i += nt) s_lvl[i] = 0;
   __syncthreads();

@@ -54,13 +54,13 @@ def flash_prefill(
         raise ValueError(f"out shape {tuple(out.shape)} != q shape {tuple(q.shape)}")
     q2, k2, v2 = _packed_view(q), _packed_view(k), _packed_view(v)
     direct = _readable_in_place(out)
-    o2 = _packed_view(out) if direct else torch.empty(B * S, Hq, d, dtype=q.dtype,
-                                                       device=q.device)
+    # a copy of the caller's out when the kernels cannot write it in place
+    o2 = _packed_view(out) if direct else _packed_view(out.contiguous().clone())
     call = FlashPrefillCall(q2, k2, v2, o2, None, max(S, 1), alpha=float(alpha),
                             attention_sink=attention_sink, window_size=window_size,
                             last_n_block=last_n_block_full, native_normalize=True,
                             min_budget=min_budget, block_size=block_size, batch=B,
-                            uniform_seq_len=S)
+                            uniform_seq_len=S, cached_workspace=True)
     call.run()
     if not direct:
         out.copy_(o2.view(B, S, Hq, d))

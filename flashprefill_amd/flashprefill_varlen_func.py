@@ -50,11 +50,13 @@ def flash_prefill_varlen_func(
     target = o
     if not (o.stride(-1) == 1 and all(s % 8 == 0 for s in o.stride()[:-1])
             and o.data_ptr() % 16 == 0):
-        o = torch.empty_like(q)
+        # the kernels write a copy of the caller's o; rows of sequences the
+        # plan skips (status flags) keep the caller's values after copy-back
+        o = torch.empty(o.shape, dtype=o.dtype, device=o.device).copy_(target)
     call = FlashPrefillCall(q, k, v, o, cu_seqlens, int(max_seq_len), alpha=float(alpha),
                             attention_sink=attention_sink, window_size=window_size,
                             last_n_block=last_n_block, native_normalize=False,
-                            block_size=block_size)
+                            block_size=block_size, cached_workspace=True)
     call.run()
     if o is not target:
         target.copy_(o)

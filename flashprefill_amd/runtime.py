@@ -18,14 +18,41 @@ _DTYPES = {torch.bfloat16: _lib.FP_DTYPE_BF16, torch.float16: _lib.FP_DTYPE_F16}
 BLOCK = 128
 
 
-def attn_key_tile() -> int:
-    """Keys per online-softmax step of the attention kernel the library runs:
-    128 for the one-workgroup-per-row kernel (default), 64 for the persistent
-    kernel (FLASHPREFILL_ATTN=persistent), the 64-key-step kernels
-    (FLASHPREFILL_ATTN=wide / pipe) and the two-group kernel, whose groups take
-    the two 64-key halves of each block (FLASHPREFILL_ATTN=duo)."""
-    import os
-    return 64 if os.environ.get("FLASHPREFILL_ATTN") in ("persistent", "wide", "pipe", "duo") else 128
+class _WorkspaceCache:
+    """One reusable workspace per (device, stream) for the operator entry
+    points, grown as needed, so that a call allocates nothing once the
+    largest shape has been seen. Work on one stream is ordered, so calls on
+    that stream can share its buffer; calls on different streams get
+    different buffers. During HIP-graph capture a fresh buffer is taken from
+    the allocator instead (it then belongs to the graph's memory pool)."""
+
+    def __init__(self):
+        self._bufs = {}
+
+    def get(self, device: torch.device, nbytes: int) -> torch.Tensor:
+        stream = torch.cuda.current_stream(device)
+        if torch.cuda.is_current_stream_capturing():
+            return torch.empty(nbytes, dtype=torch.uint8, device=device)
+        key = (device.index, stream.cuda_stream)
+        buf = self._bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            grow = nbytes if buf is None else max(nbytes, buf.numel() + buf.numel() // 2)
+            self._bufs[key] = buf = None
+            buf = torch.empty(grow, dtype=torch.uint8, device=device)
+            self._bufs[key] = buf
+        return buf
+
+    def clear(self) -> None:
+        self._bufs.clear()
+
+
+WORKSPACES = _WorkspaceCache()
+
+
+def release_workspaces() -> None:
+    """Drop the cached operator workspaces (their memory returns to torch's
+    caching allocator)."""
+    WORKSPACES.clear()
 
 
 def _dtype_code(t: torch.Tensor) -> int:
@@ -40,6 +67,8 @@ class FlashPrefillCall:
 
     ``cu_seqlens`` is a device int32 tensor of B+1 offsets, or None for
     ``batch`` sequences of ``uniform_seq_len`` tokens (the batched layout).
+    The workspace is ``workspace`` when given, else the stream's cached one
+    when ``cached_workspace`` is set, else a new allocation.
     """
 
     def __init__(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
@@ -47,7 +76,8 @@ class FlashPrefillCall:
                  attention_sink: int = 2, window_size: int = 4, last_n_block: int = 2,
                  native_normalize: bool = False, min_budget: int = 0,
                  block_size: int = BLOCK, batch: Optional[int] = None,
-                 uniform_seq_len: int = 0, workspace: Optional[torch.Tensor] = None):
+                 uniform_seq_len: int = 0, workspace: Optional[torch.Tensor] = None,
+                 cached_workspace: bool = False):
         for name, t in (("q", q), ("k", k), ("v", v), ("o", o)):
             if t.dim() != 3:
                 raise ValueError(f"{name} must be (tokens, heads, head_dim), got {tuple(t.shape)}")
@@ -96,6 +126,8 @@ class FlashPrefillCall:
         L = _lib.FpWsLayout()
         _lib.check(self.lib.fp_workspace_layout(ctypes.byref(P), ctypes.byref(L)))
         self.layout = L
+        if workspace is None and cached_workspace:
+            workspace = WORKSPACES.get(self.device, L.total_bytes)
         if workspace is None or workspace.numel() < L.total_bytes:
             workspace = torch.empty(L.total_bytes, dtype=torch.uint8, device=self.device)
         self.workspace = workspace
@@ -176,6 +208,13 @@ class FlashPrefillCall:
         L = self.layout
         return self._view(L.idx_off, torch.int32, self.Hq * L.tri_cap).view(self.Hq, L.tri_cap)
 
+    def _row_slots(self, b: int, tile, tri):
+        """Triangular slot table of sequence b: for every (q-block i, slot n <= i)
+        the flat list position tri[b] + i(i+1)/2 + n, with i and n."""
+        nb = tile[b + 1] - tile[b]
+        r, c = torch.tril_indices(nb, nb)
+        return nb, r, c, tri[b] + r * (r + 1) // 2 + c
+
     def selection_masks(self) -> List[torch.Tensor]:
         """Per-sequence (Hq, NB, NB) bool masks rebuilt from the index lists (CPU)."""
         tile, tri, _, _ = self.seq_tables()
@@ -183,31 +222,36 @@ class FlashPrefillCall:
         idx = self.index_lists().cpu()
         out = []
         for b in range(self.batch):
-            nb = tile[b + 1] - tile[b]
+            nb, r, c, pos = self._row_slots(b, tile, tri)
             mask = torch.zeros(self.Hq, nb, nb, dtype=torch.bool)
-            for i in range(nb):
-                base = tri[b] + i * (i + 1) // 2
-                for h in range(self.Hq):
-                    c = int(cnt[h, tile[b] + i])
-                    if c:
-                        mask[h, i, idx[h, base:base + c].long()] = True
+            for h in range(self.Hq):
+                valid = c < cnt[h, tile[b] + r]
+                j = idx[h, pos[valid]].long()
+                if j.numel() and (j.min() < 0 or j.max() >= nb):
+                    raise AssertionError(f"index list entry outside [0, {nb}) in sequence {b}")
+                mask[h].index_put_((r[valid], j), torch.ones((), dtype=torch.bool))
             out.append(mask)
         return out
 
     def ordered_lists_ok(self) -> bool:
-        """True when every row's list is strictly ascending (CPU check)."""
+        """True when every row's list is strictly ascending and its count is
+        within the row's i + 1 slots (CPU check)."""
         tile, tri, _, _ = self.seq_tables()
         cnt = self.counts().cpu()
         idx = self.index_lists().cpu()
         for b in range(self.batch):
-            nb = tile[b + 1] - tile[b]
-            for i in range(nb):
-                base = tri[b] + i * (i + 1) // 2
-                for h in range(self.Hq):
-                    c = int(cnt[h, tile[b] + i])
-                    row = idx[h, base:base + c]
-                    if c > 1 and not bool((row[1:] > row[:-1]).all()):
-                        return False
+            nb, r, c, pos = self._row_slots(b, tile, tri)
+            if nb == 0:
+                continue
+            rows = cnt[:, tile[b]:tile[b + 1]]
+            if bool((rows < 0).any()) or bool((rows > torch.arange(1, nb + 1)).any()):
+                return False
+            for h in range(self.Hq):
+                # consecutive valid slots n-1, n of one row must ascend
+                valid = (c >= 1) & (c < cnt[h, tile[b] + r])
+                p1 = pos[valid]
+                if p1.numel() and not bool((idx[h, p1] > idx[h, p1 - 1]).all()):
+                    return False
         return True
 
     def tri_scores(self, scores: Sequence[torch.Tensor]) -> torch.Tensor:

@@ -51,7 +51,9 @@ extern "C" {
  * fp_read_status): set by the kernels when cu_seqlens disagrees with the host
  * sizes; the affected sequences are skipped and their output left untouched. */
 #define FP_STATUS_SEQ_TOO_LONG 1u   /* a sequence is longer than max_seq_len */
-#define FP_STATUS_BAD_CU_SEQLENS 2u /* cu_seqlens decreasing or beyond total_tokens */
+#define FP_STATUS_BAD_CU_SEQLENS 2u /* a sequence outside [0, total_tokens], of negative
+                                        length, or starting before an earlier cu_seqlens
+                                        entry (it would overlap a kept sequence) */
 
 typedef struct fp_problem {
     /* Q (T, Hq, d), K/V (T, Hkv, d), O (T, Hq, d): device pointers, head dim
@@ -105,7 +107,6 @@ typedef struct fp_ws_layout {
     size_t items_off;    /* nb_sum_cap records of 32 bytes, heaviest first:
                             int32 b, i, seq_len, seq_tile[b] + i;
                             int64 seq_start, seq_tri[b] + i (i + 1) / 2 */
-    size_t sched_off;    /* int32[16]: attention work-queue counters */
     size_t mk_off;
     size_t cnt_off;
     size_t idx_off;

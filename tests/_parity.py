@@ -9,7 +9,7 @@ from typing import List, Optional, Sequence
 
 import torch
 
-from flashprefill_amd.runtime import FlashPrefillCall, attn_key_tile
+from flashprefill_amd.runtime import FlashPrefillCall
 from oracle import flashprefill_oracle as O
 
 OUT_MAX_ABS = 2e-2   # north-star output tolerance (bf16)
@@ -47,9 +47,12 @@ def seq_slices(cu: Sequence[int]):
 
 def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n=2,
                native=False, check_oracle_scores=True, attention=True,
-               min_budget=0) -> StageReport:
+               min_budget=0, attn_rows=None) -> StageReport:
     """Run plan/pool/search(dump)/select/attn on the GPU and compare each stage
-    with the oracle. q/k/v are CPU tensors (T, H, d); cu_list python ints."""
+    with the oracle. q/k/v are CPU tensors (T, H, d); cu_list python ints.
+    ``attn_rows`` {sequence: [(head, q-block), ...]} restricts the attention
+    comparison to those rows (the oracle's attention over the GPU's lists of
+    just those rows), for sequences whose full oracle attention is slow."""
     dev = torch.device("cuda:0")
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
     od = torch.full_like(qd, float("nan"))
@@ -124,11 +127,82 @@ def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n
         for b, (s0, s1) in enumerate(seq_slices(cu_list)):
             if s1 == s0:
                 continue
-            ref = O.sparse_attention(q[s0:s1], k[s0:s1], v[s0:s1], gpu_sel[b],
-                                     k_tile=attn_key_tile())
-            diffs.append((out[s0:s1].float() - ref.float()).abs().reshape(-1))
+            if attn_rows is None:
+                ref = O.sparse_attention(q[s0:s1], k[s0:s1], v[s0:s1], gpu_sel[b])
+                diffs.append((out[s0:s1].float() - ref.float()).abs().reshape(-1))
+                continue
+            sub = torch.zeros_like(gpu_sel[b])
+            for h, i in attn_rows.get(b, []):
+                sub[h, i] = gpu_sel[b][h, i]
+            ref = O.sparse_attention(q[s0:s1], k[s0:s1], v[s0:s1], sub)
+            for h, i in attn_rows.get(b, []):
+                r0, r1 = i * 128, min((i + 1) * 128, s1 - s0)
+                diffs.append((out[s0 + r0:s0 + r1, h].float() - ref[r0:r1, h].float())
+                             .abs().reshape(-1))
         d = torch.cat(diffs)
         assert not torch.isnan(d).any(), "NaN in GPU output"
         rep.out_max_abs = d.max().item()
         rep.out_mean_abs = d.mean().item()
     return rep
+
+
+def oracle_head_scores(q_seq, mk, h):
+    """The oracle's fp32 block scores (p, m) of query head h alone, from pooled
+    keys ``mk`` (NB, Hkv, d): (1, NB, NB) each."""
+    G = q_seq.shape[1] // mk.shape[1]
+    return O.block_score(q_seq[:, h:h + 1], mk[:, h // G:h // G + 1])
+
+
+def check_every_row_selection(call, q_cpu, k_cpu, *, native, alpha, sink=2, window=4, last_n=2,
+                              min_budget=0, oracle_heads=None):
+    """Selection parity on every (head, sequence, q-block) row of a call whose
+    plan and pooling stages have run: the search kernel's fp32 scores are
+    dumped, and the oracle's selection from those scores must equal the GPU's
+    index lists on every row. Then, for the (sequence, head) pairs in
+    ``oracle_heads``, the GPU selection kernel is fed the oracle's own fp32
+    scores (computed from the oracle's pooled K) and must reproduce the
+    oracle's selection exactly (all other heads keep the GPU's scores).
+    Returns (rows checked, selected cells)."""
+    dump_p, dump_m = call.search(dump=True)
+    torch.cuda.synchronize()
+    assert call.status() == 0
+    assert call.ordered_lists_ok()
+    tile, tri, start, lens = call.seq_tables()
+    gpu_sel = call.selection_masks()
+    gp = call.untri_scores(dump_p)
+    gm = call.untri_scores(dump_m)
+    rows = selected = 0
+    for b, L in enumerate(lens):
+        nb = gp[b].shape[-1]
+        if nb == 0:
+            assert L == 0
+            continue
+        tril = torch.tril(torch.ones(nb, nb, dtype=torch.bool))
+        want = O.select_from_scores(gp[b].nan_to_num(0.0).where(tril, torch.zeros(())),
+                                    gm[b].where(tril, torch.tensor(float("-inf"))),
+                                    native, alpha, sink, window, last_n, min_budget)
+        bad = int((want != gpu_sel[b]).sum())
+        assert bad == 0, f"sequence {b}: {bad} cells differ from the oracle's selection of the GPU scores"
+        rows += gpu_sel[b].shape[0] * nb
+        selected += int(gpu_sel[b].sum())
+    if oracle_heads:
+        p_in = [x.clone() for x in gp]
+        m_in = [x.clone() for x in gm]
+        wants = {}
+        for b, h in oracle_heads:
+            t0, L = start[b], lens[b]
+            mk_o = O.pool_k(k_cpu[t0:t0 + L])
+            p_o, m_o = oracle_head_scores(q_cpu[t0:t0 + L], mk_o, h)
+            p_in[b][h] = p_o[0]
+            m_in[b][h] = m_o[0]
+            wants[(b, h)] = O.select_from_scores(p_o, m_o, native, alpha, sink, window, last_n,
+                                                 min_budget)[0]
+        call.select(call.tri_scores([x.nan_to_num(0.0) for x in p_in]),
+                    call.tri_scores([x.nan_to_num(float("-inf")) for x in m_in]))
+        torch.cuda.synchronize()
+        sel2 = call.selection_masks()
+        for (b, h), want in wants.items():
+            bad = int((sel2[b][h] != want).sum())
+            assert bad == 0, f"sequence {b} head {h}: GPU selection of the oracle's scores differs in {bad} cells"
+        call.search()  # restore the GPU's own lists
+    return rows, selected

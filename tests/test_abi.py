@@ -63,7 +63,7 @@ def test_layout_bounds():
     cap = L.nb_sum_cap
     assert L.tri_cap == (cap // 32) * 32 * 33 // 2 + (cap % 32) * (cap % 32 + 1) // 2
     offs = [L.status_off, L.seq_tile_off, L.seq_tri_off, L.seq_start_off, L.seq_len_off,
-            L.items_off, L.sched_off, L.mk_off, L.cnt_off, L.idx_off]
+            L.items_off, L.mk_off, L.cnt_off, L.idx_off]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
     assert L.total_bytes >= L.idx_off + 4 * 8 * L.tri_cap
     assert _lib.load().fp_workspace_bytes(ctypes.byref(_problem())) == L.total_bytes
@@ -155,3 +155,55 @@ def test_class_level_forwards_map_arguments_like_the_reference(monkeypatch):
         FlashPrefill.apply(q, k, v, o, 128, 64)
     with pytest.raises(ValueError):
         FlashPrefill_varlen.apply(q, k, v, o, cu, 4096, 128, 64)
+
+
+def _plan_block_count(cu, total, max_len, reject_overlap=True):
+    """The plan kernel's per-sequence rule restated on the host: sequences
+    outside [0, total], of negative length or (with ``reject_overlap``)
+    starting before an earlier cu_seqlens entry are skipped, as are those
+    longer than max_len; returns (sum NB, sum NB (NB + 1) / 2) of the kept."""
+    nb_sum = tri_sum = 0
+    run_max = None
+    for b in range(len(cu) - 1):
+        start, end = cu[b], cu[b + 1]
+        run_max = start if run_max is None else max(run_max, start)
+        n = end - start
+        if start < 0 or n < 0 or end > total or (reject_overlap and run_max > start):
+            continue
+        if n > max_len:
+            continue
+        nb = (n + 127) // 128
+        nb_sum += nb
+        tri_sum += nb * (nb + 1) // 2
+    return nb_sum, tri_sum
+
+
+def test_plan_rule_keeps_block_count_within_workspace_capacity():
+    # [0, T, 0, T]: checking each sequence on its own keeps sequences 0 and 2
+    # (2048 blocks at T = 131072, twice the capacity); rejecting a sequence
+    # that starts before an earlier entry keeps only sequence 0
+    T = 131072
+    rc, L = _layout(_problem(batch=3, max_seq_len=T, total_tokens=T))
+    assert rc == _lib.FP_OK
+    cu = [0, T, 0, T]
+    assert _plan_block_count(cu, T, T, reject_overlap=False)[0] == 2048 > L.nb_sum_cap
+    nb_sum, tri_sum = _plan_block_count(cu, T, T)
+    assert nb_sum == 1024 <= L.nb_sum_cap and tri_sum <= L.tri_cap
+
+
+def test_plan_rule_bound_holds_for_arbitrary_cu_seqlens():
+    # any int32 cu_seqlens (decreasing, negative, overlapping, past the end):
+    # the kept sequences never need more than the layout's capacities
+    import random
+    rnd = random.Random(5)
+    for _ in range(2000):
+        B = rnd.randint(1, 12)
+        T = rnd.randint(0, 5000)
+        max_len = rnd.randint(1, 4000)
+        cu = [rnd.choice([rnd.randint(-50, T + 50), rnd.randint(0, T)]) for _ in range(B + 1)]
+        if rnd.random() < 0.5:
+            cu = sorted(cu)
+        rc, L = _layout(_problem(batch=B, max_seq_len=max_len, total_tokens=T))
+        assert rc == _lib.FP_OK
+        nb_sum, tri_sum = _plan_block_count(cu, T, max_len)
+        assert nb_sum <= L.nb_sum_cap and tri_sum <= L.tri_cap, (cu, T, max_len)

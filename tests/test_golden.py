@@ -55,7 +55,7 @@ def test_oracle_reproduces_golden(name):
 @pytest.mark.gpu
 @pytest.mark.parametrize("name", ["varlen_bf16_ragged", "native_bf16_b2"])
 def test_gpu_matches_golden(name):
-    from flashprefill_amd.runtime import FlashPrefillCall, attn_key_tile
+    from flashprefill_amd.runtime import FlashPrefillCall
     q, k, v, cu, out, traces = _load(name)
     dev = torch.device("cuda:0")
     lens = [cu[b + 1] - cu[b] for b in range(len(cu) - 1)]
@@ -73,7 +73,7 @@ def test_gpu_matches_golden(name):
     assert flips <= max(2, cells // 500)
     # output against the oracle's attention over the GPU's own selection
     ref = torch.cat([O.sparse_attention(q[cu[b]:cu[b + 1]], k[cu[b]:cu[b + 1]],
-                                        v[cu[b]:cu[b + 1]], sels[b], k_tile=attn_key_tile())
+                                        v[cu[b]:cu[b + 1]], sels[b])
                      for b in range(len(lens))])
     d = (o.cpu().float() - ref.float()).abs()
     assert d.max().item() <= OUT_MAX_ABS and d.mean().item() <= OUT_MEAN_ABS

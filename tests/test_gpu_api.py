@@ -105,12 +105,9 @@ def test_all_blocks_selected_is_dense_causal():
     _close(o, ref.permute(1, 0, 2))
 
 
-@pytest.mark.parametrize("kernel", ["rows", "persistent", "wide", "pipe", "duo"])
-def test_all_blocks_selected_long_rows(kernel, monkeypatch):
-    # 8300 tokens: 65 blocks per row (the wide kernel reloads its 64-entry
-    # block-list chunk), a partial last block of 108 rows (its second half tile
-    # holds 44), dense causal attention against fp32 SDPA
-    monkeypatch.setenv("FLASHPREFILL_ATTN", kernel)
+def test_all_blocks_selected_long_rows():
+    # 8300 tokens: 65 blocks per row, a partial last block of 108 rows, dense
+    # causal attention against fp32 SDPA
     T, Hq, Hkv, d = 8300, 4, 1, 128
     q, k, v = _rand((T, Hq, d), 21, scale=1.5), _rand((T, Hkv, d), 22, scale=1.5), _rand((T, Hkv, d), 23)
     o = torch.empty(T, Hq, d, dtype=torch.bfloat16, device=DEV)
@@ -124,14 +121,12 @@ def test_all_blocks_selected_long_rows(kernel, monkeypatch):
     _close(o, ref.permute(1, 0, 2).cpu())
 
 
-@pytest.mark.parametrize("kernel", ["rows", "persistent", "wide", "pipe", "duo"])
-def test_growing_logits_rescale_every_block(kernel, monkeypatch):
+def test_growing_logits_rescale_every_block():
     # every key block's logits exceed the previous block's by ~9 log2 units
     # (more than the kernels' rescaling slack of 8), so the running max moves
     # and the output accumulators are rescaled on every block; the last
     # query rows then attend almost only to their own (diagonal) block.
     # All blocks selected (alpha 0): dense causal attention vs fp32 SDPA.
-    monkeypatch.setenv("FLASHPREFILL_ATTN", kernel)
     T, Hq, Hkv, d = 2048, 2, 1, 128
     g = torch.Generator().manual_seed(31)
     e = torch.zeros(d)
@@ -165,6 +160,33 @@ def test_status_flags_and_untouched_output():
     call = FlashPrefillCall(q, k, v, o, cu_bad, 2000, alpha=0.18)
     call.run()
     assert call.status() & _lib.FP_STATUS_BAD_CU_SEQLENS
+    # overlapping sequences [0, T, 0, T]: the second has negative length and
+    # the third starts before an earlier entry, so both are skipped and the
+    # block count stays within the workspace capacity; the first sequence's
+    # output equals a call on [0, T] alone
+    o_ov = torch.full((T, Hq, d), 7.0, dtype=torch.bfloat16, device=DEV)
+    cu_ov = torch.tensor([0, T, 0, T], dtype=torch.int32, device=DEV)
+    call = FlashPrefillCall(q, k, v, o_ov, cu_ov, T, alpha=0.18)
+    call.run()
+    assert call.status() == _lib.FP_STATUS_BAD_CU_SEQLENS
+    tile, tri, start, lens = call.seq_tables()
+    assert lens == [T, 0, 0]
+    assert tile[-1] == (T + 127) // 128 <= call.layout.nb_sum_cap
+    o_one = torch.full((T, Hq, d), 7.0, dtype=torch.bfloat16, device=DEV)
+    FlashPrefillCall(q, k, v, o_one, torch.tensor([0, T], dtype=torch.int32, device=DEV), T,
+                     alpha=0.18).run()
+    torch.cuda.synchronize()
+    assert torch.equal(o_ov, o_one)
+    # a sequence skipped by the plan keeps the caller's output rows also when
+    # o is not writable in place (the operator writes a copy and copies back)
+    flat = torch.full((T * Hq * d + 4,), 7.0, dtype=torch.bfloat16, device=DEV)
+    o_view = flat[4:].view(T, Hq, d)  # 8-byte aligned: not writable in place
+    assert o_view.data_ptr() % 16 != 0
+    flash_prefill_varlen_func(q, k, v, o_view, torch.tensor([0, 300, 1000], dtype=torch.int32,
+                              device=DEV), 512, 0.18)
+    torch.cuda.synchronize()
+    assert (o_view[300:] == 7.0).all()
+    assert not (o_view[:300] == 7.0).all()
 
 
 def test_error_paths():

@@ -1,10 +1,17 @@
-"""Parity at the full config-3 size (131072 tokens, 32 q / 8 kv heads,
-d = 128, bf16; and one 262144-token sequence for the default kernel): the whole operator runs on the GPU through the C ABI, and a
-sample of (head, q-block) rows from light to heavy is recomputed by the
-oracle's row pipeline (pooled K of all blocks, scores, normalisation,
-selection, attention). The selection lists must agree (threshold flips are
-counted and at most one is allowed), the outputs must be within the bf16
-tolerance, and two runs must be bit-identical."""
+"""Parity at full size: config 3 (131072 tokens, 32 q / 8 kv heads, d = 128,
+bf16), one 262144-token sequence, config 4 (Qwen2.5 shapes, ragged
+{256K, 64K, 17K, 3K, 1K}) and one sequence of the maximum length (1,048,576
+tokens, the search's largest LDS footprint).
+
+Two checks per case:
+* every row's selection: the search kernel's fp32 scores are dumped and the
+  oracle's selection from them must equal the GPU's index lists on every
+  (head, sequence, q-block) row; for sampled heads the GPU selection fed the
+  oracle's own scores must equal the oracle's selection;
+* sampled rows end to end: the oracle's row pipeline (pooled K of all
+  blocks, scores, normalisation, selection, attention) against the GPU's
+  lists (threshold flips counted, at most one allowed) and output (bf16
+  tolerance), and two full runs bit-identical."""
 
 import pytest
 import torch
@@ -12,85 +19,98 @@ import torch
 from flashprefill_amd import synth
 from flashprefill_amd.runtime import FlashPrefillCall
 from oracle import flashprefill_oracle as O
-from tests._parity import OUT_MAX_ABS, OUT_MEAN_ABS
+from tests._parity import OUT_MAX_ABS, OUT_MEAN_ABS, check_every_row_selection
 
 pytestmark = pytest.mark.gpu
 
-S = 131072
 ALPHA = 0.18
-ROWS = [(0, 1023), (5, 1000), (13, 777), (31, 512), (7, 300), (20, 64), (26, 2), (9, 0)]
 
 
-@pytest.fixture(scope="module")
-def case():
-    spec = synth.llama_spec(S, seed=128)
-    q, k, v, cu = synth.make_inputs(spec, device="cuda:0")
-    qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
-    ref = O.flashprefill_rows(qc, kc, vc, ROWS, alpha=ALPHA, attention_sink=2, window=4,
-                              last_n=2, native=False)
-    return q, k, v, cu, ref
-
-
-def _check_sampled_rows(S, q, k, v, cu, ref, label):
-    outs = []
-    for _ in range(2):
-        o = torch.full_like(q, float("nan"))
-        call = FlashPrefillCall(q, k, v, o, cu, S, alpha=ALPHA, attention_sink=2,
-                                window_size=4, last_n_block=2)
-        call.run()
-        torch.cuda.synchronize()
-        assert call.status() == 0
-        outs.append(o)
-    assert torch.equal(outs[0], outs[1]), "two runs differ"
-    out = outs[0]
-    assert not torch.isnan(out).any(), "unwritten output rows"
-    nb = S // 128
-    tile, tri, _, _ = call.seq_tables()
+def _sampled_rows(call, out, b, S, ref, label):
+    """Compare the GPU's lists and output of sequence b with the oracle's
+    row pipeline on the rows in ``ref``; returns (flips, rows checked)."""
+    tile, tri, start, _ = call.seq_tables()
+    t0 = start[b]
     cnt = call.counts().cpu()
     idx = call.index_lists().cpu()
+    nb = (S + 127) // 128
     flips, checked = 0, 0
     for (h, i), (sel_o, out_o) in ref.items():
-        c = int(cnt[h, tile[0] + i])
-        base = tri[0] + i * (i + 1) // 2
+        c = int(cnt[h, tile[b] + i])
+        base = tri[b] + i * (i + 1) // 2
         lst = idx[h, base:base + c]
-        assert bool((lst[1:] > lst[:-1]).all()), f"row {(h, i)} list not ascending"
+        assert bool((lst[1:] > lst[:-1]).all()), f"{label} row {(h, i)} list not ascending"
         gsel = torch.zeros(nb, dtype=torch.bool)
         gsel[lst.long()] = True
         row_flips = int((gsel != sel_o).sum())
         flips += row_flips
         if row_flips:
             continue  # the oracle output is for a different block set
-        d = (out[i * 128:(i + 1) * 128, h].float().cpu() - out_o.float()).abs()
-        print(f"  row {(h, i)}: {c} blocks, out max {d.max().item():.2e} mean {d.mean().item():.2e}",
-              flush=True)
+        q0, q1 = t0 + i * 128, t0 + min((i + 1) * 128, S)
+        d = (out[q0:q1, h].float().cpu() - out_o.float()).abs()
+        print(f"  {label} row {(h, i)}: {c} blocks, out max {d.max().item():.2e} "
+              f"mean {d.mean().item():.2e}", flush=True)
         assert d.max().item() <= OUT_MAX_ABS
         assert d.mean().item() <= OUT_MEAN_ABS
         checked += 1
+    return flips, checked
+
+
+def _run_twice(q, k, v, cu, max_len, alpha):
+    outs = []
+    for _ in range(2):
+        o = torch.full_like(q, float("nan"))
+        call = FlashPrefillCall(q, k, v, o, cu, max_len, alpha=alpha, attention_sink=2,
+                                window_size=4, last_n_block=2)
+        call.run()
+        torch.cuda.synchronize()
+        assert call.status() == 0
+        outs.append(o)
+    assert torch.equal(outs[0], outs[1]), "two runs differ"
+    assert not torch.isnan(outs[0]).any(), "unwritten output rows"
+    return call, outs[0]
+
+
+def _full_case(S, seed, rows, oracle_heads, label, every_row=True, spec=None):
+    spec = spec or synth.llama_spec(S, seed=seed)
+    print(f"\n  {label}: S={S} Hq={spec.num_q_heads} Hkv={spec.num_kv_heads} d={spec.head_dim} "
+          f"seed={spec.seed}", flush=True)
+    q, k, v, cu = synth.make_inputs(spec, device="cuda:0")
+    call, out = _run_twice(q, k, v, cu, S, ALPHA)
+    qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
+    if every_row:
+        n_rows, n_sel = check_every_row_selection(call, qc, kc, native=False, alpha=ALPHA,
+                                                  oracle_heads=[(0, h) for h in oracle_heads])
+        print(f"  {label}: every row's selection matches ({n_rows} cells, {n_sel} selected)",
+              flush=True)
+    ref = O.flashprefill_rows(qc, kc, vc, rows, alpha=ALPHA, attention_sink=2, window=4,
+                              last_n=2, native=False)
+    flips, checked = _sampled_rows(call, out, 0, S, ref, label)
     print(f"  {label}: threshold flips {flips}, rows checked {checked}/{len(ref)}", flush=True)
     assert flips <= 1
     assert checked >= len(ref) - 1
 
 
-@pytest.mark.parametrize("kernel", ["rows", "persistent", "wide", "pipe", "duo"])
-def test_128k_sampled_rows_match_oracle_and_runs_are_identical(case, kernel, monkeypatch):
-    monkeypatch.setenv("FLASHPREFILL_ATTN", kernel)
-    q, k, v, cu, ref = case
-    _check_sampled_rows(S, q, k, v, cu, ref, kernel)
+def test_128k_every_row_selection_and_sampled_rows():
+    rows = [(0, 1023), (5, 1000), (13, 777), (31, 512), (7, 300), (20, 64), (26, 2), (9, 0)]
+    _full_case(131072, 128, rows, oracle_heads=[7], label="128K")
 
 
-S256 = 262144
-ROWS256 = [(0, 2047), (17, 1800), (4, 1024), (29, 300), (11, 5), (22, 0)]
+def test_256k_sampled_rows():
+    # 2048 blocks per row: the search's p / m arrays take 16 KB of LDS and the
+    # lists are twice as long
+    rows = [(0, 2047), (17, 1800), (4, 1024), (29, 300), (11, 5), (22, 0)]
+    _full_case(262144, 256, rows, oracle_heads=[], label="256K", every_row=False)
 
 
-def test_256k_sampled_rows_match_oracle_and_runs_are_identical(monkeypatch):
-    # 2048 blocks per row: the search's p / m arrays take 16 KB of LDS (three
-    # workgroups per CU instead of four) and the lists are twice as long
-    monkeypatch.delenv("FLASHPREFILL_ATTN", raising=False)
-    spec = synth.llama_spec(S256, seed=256)
-    q, k, v, cu = synth.make_inputs(spec, device="cuda:0")
-    ref = O.flashprefill_rows(q.cpu(), k.cpu(), v.cpu(), ROWS256, alpha=ALPHA, attention_sink=2,
-                              window=4, last_n=2, native=False)
-    _check_sampled_rows(S256, q, k, v, cu, ref, "rows at 256K")
+def test_max_length_sequence_sampled_rows():
+    # 1,048,576 tokens = 8192 blocks, the largest max_seq_len: the search
+    # kernel needs 96 KB of dynamic LDS at d = 128 (set through the function
+    # attribute), and the plan tables hold 8192 levels
+    S = 1 << 20
+    spec = synth.SynthSpec(seq_lens=(S,), num_q_heads=2, num_kv_heads=1, head_dim=128, seed=20)
+    rows = [(0, 8191), (1, 8000), (0, 4096), (1, 1000), (0, 3)]
+    _full_case(S, 20, rows, oracle_heads=[], label="1M", every_row=False, spec=spec)
 
 
 # config 4 at full size: Qwen2.5 shapes (28 q / 4 kv heads), ragged batch
@@ -99,42 +119,32 @@ ROWS_VARLEN = {0: [(3, 2047), (27, 900), (10, 1)], 1: [(14, 511), (0, 40)],
                2: [(20, 135), (7, 3)], 3: [(25, 23)], 4: [(1, 7), (18, 0)]}
 
 
-def test_config4_ragged_batch_sampled_rows_match_oracle(monkeypatch):
-    monkeypatch.delenv("FLASHPREFILL_ATTN", raising=False)
+def test_config4_every_row_selection_and_sampled_rows():
     spec = synth.qwen_varlen_spec()
     q, k, v, cu = synth.make_inputs(spec, device="cuda:0")
+    alpha = 0.08
     o = torch.full_like(q, float("nan"))
-    call = FlashPrefillCall(q, k, v, o, cu, max(spec.seq_lens), alpha=0.08, attention_sink=2,
+    call = FlashPrefillCall(q, k, v, o, cu, max(spec.seq_lens), alpha=alpha, attention_sink=2,
                             window_size=4, last_n_block=2)
     call.run()
     torch.cuda.synchronize()
     assert call.status() == 0
     assert not torch.isnan(o).any(), "unwritten output rows"
-    tile, tri, start, _ = call.seq_tables()
-    cnt = call.counts().cpu()
-    idx = call.index_lists().cpu()
+    qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
+    n_rows, n_sel = check_every_row_selection(call, qc, kc, native=False, alpha=alpha,
+                                              oracle_heads=[(1, 9), (3, 20)])
+    print(f"\n  config 4: every row's selection matches ({n_rows} cells, {n_sel} selected)",
+          flush=True)
+    _, _, start, _ = call.seq_tables()
     flips, checked, total = 0, 0, 0
     for b, rows in ROWS_VARLEN.items():
         t0, S = start[b], spec.seq_lens[b]
-        ref = O.flashprefill_rows(q[t0:t0 + S].cpu(), k[t0:t0 + S].cpu(), v[t0:t0 + S].cpu(), rows,
-                                  alpha=0.08, attention_sink=2, window=4, last_n=2, native=False)
-        nb = (S + 127) // 128
-        for (h, i), (sel_o, out_o) in ref.items():
-            total += 1
-            c = int(cnt[h, tile[b] + i])
-            base = tri[b] + i * (i + 1) // 2
-            lst = idx[h, base:base + c]
-            assert bool((lst[1:] > lst[:-1]).all()), f"row {(b, h, i)} list not ascending"
-            gsel = torch.zeros(nb, dtype=torch.bool)
-            gsel[lst.long()] = True
-            row_flips = int((gsel != sel_o).sum())
-            flips += row_flips
-            if row_flips:
-                continue
-            d = (o[t0 + i * 128:t0 + min((i + 1) * 128, S), h].float().cpu() - out_o.float()).abs()
-            assert d.max().item() <= OUT_MAX_ABS
-            assert d.mean().item() <= OUT_MEAN_ABS
-            checked += 1
+        ref = O.flashprefill_rows(qc[t0:t0 + S], kc[t0:t0 + S], vc[t0:t0 + S], rows, alpha=alpha,
+                                  attention_sink=2, window=4, last_n=2, native=False)
+        f, c = _sampled_rows(call, o, b, S, ref, f"config 4 seq {b}")
+        flips += f
+        checked += c
+        total += len(ref)
     print(f"  config 4: threshold flips {flips}, rows checked {checked}/{total}", flush=True)
     assert flips <= 1
     assert checked >= total - 1

@@ -20,17 +20,6 @@ from tests._parity import OUT_MAX_ABS, OUT_MEAN_ABS, run_stages
 
 pytestmark = pytest.mark.gpu
 
-# the attention kernels: one workgroup per row (default), the persistent one and
-# the 64-queries-per-wave one
-KERNELS = ["rows", "persistent", "wide", "pipe", "duo"]
-
-
-@pytest.fixture(params=KERNELS)
-def attn_kernel(request, monkeypatch):
-    monkeypatch.setenv("FLASHPREFILL_ATTN", request.param)
-    return request.param
-
-
 def _check(rep, max_flip_frac=2e-3):
     print(f"\n  pool_ulp={rep.pool_ulp} m_rel={rep.m_max_rel:.2e} p_rel={rep.p_max_rel:.2e} "
           f"sel_mismatch(gpu scores)={rep.sel_from_gpu_scores_mismatch} "
@@ -60,19 +49,19 @@ def _rand_inputs(lens, Hq, Hkv, d, dtype, seed, scale=1.0):
 
 
 @pytest.mark.parametrize("native", [False, True])
-def test_ragged_varlen_bf16(native, attn_kernel):
+def test_ragged_varlen_bf16(native):
     lens = [300, 128, 1, 640, 129]
     q, k, v, cu = _rand_inputs(lens, 8, 2, 128, torch.bfloat16, 1, scale=1.5)
     _check(run_stages(q, k, v, cu, max(lens), alpha=0.18, native=native))
 
 
-def test_llama_4k_structured(attn_kernel):
+def test_llama_4k_structured():
     spec = synth.llama_spec(4096, seed=4)
     q, k, v, cu = synth.make_inputs(spec)
     _check(run_stages(q, k, v, cu.tolist(), 4096, alpha=0.18))
 
 
-def test_qwen_heads_not_multiple_of_8_fp16_d64(attn_kernel):
+def test_qwen_heads_not_multiple_of_8_fp16_d64():
     lens = [1000, 555]
     q, k, v, cu = _rand_inputs(lens, 28, 4, 64, torch.float16, 2, scale=1.2)
     _check(run_stages(q, k, v, cu, 1000, alpha=0.08))
@@ -95,3 +84,34 @@ def test_selection_params_sweep():
                                         (0.12, 5, 2, 3)]:
         _check(run_stages(q, k, v, cu, 1024, alpha=alpha, sink=sink, window=window,
                           last_n=last_n, attention=(alpha != 0.0)))
+
+
+@pytest.mark.parametrize("S,seed", [(16384, 16), (32768, 32)])
+def test_config2_llama_16k_32k(S, seed):
+    # config 2 at its longer lengths: every stage against the oracle on all
+    # rows (pooled K, scores, selection both ways, flips); the attention
+    # output on sampled rows from light to heavy
+    spec = synth.llama_spec(S, seed=seed)
+    q, k, v, cu = synth.make_inputs(spec)
+    nb = S // 128
+    rows = {0: [(0, nb - 1), (9, nb - 3), (17, nb // 2), (31, nb // 4), (4, 7), (23, 0)]}
+    _check(run_stages(q, k, v, cu.tolist(), S, alpha=0.18, attn_rows=rows))
+
+
+def test_config1_shape_bf16():
+    # config 1's shapes and input distribution (4096 tokens, 8 q / 2 kv heads,
+    # d = 64, unscaled N(0, 1), K rows 0-3 x4, 16 stripe columns, seed 0) in
+    # bf16, every stage against the full oracle, at the Llama alpha and the
+    # reference class default
+    from dataclasses import replace
+    spec = replace(synth.config1_spec(seed=0), dtype=torch.bfloat16)
+    q, k, v, cu = synth.make_inputs(spec)
+    for alpha in (0.18, 0.7):
+        _check(run_stages(q, k, v, cu.tolist(), 4096, alpha=alpha))
+
+
+def test_zero_length_sequences_in_a_ragged_batch():
+    # empty sequences at the start, in the middle and at the end of the batch
+    lens = [0, 300, 0, 128, 1, 0, 640, 0]
+    q, k, v, cu = _rand_inputs(lens, 8, 2, 128, torch.bfloat16, 3, scale=1.5)
+    _check(run_stages(q, k, v, cu, max(lens), alpha=0.18))
