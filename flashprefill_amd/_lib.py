@@ -29,8 +29,9 @@ ABI_VERSION = 3
 EXPORTS = (
     "fp_workspace_layout", "fp_workspace_bytes", "fp_flashprefill", "fp_plan", "fp_pool_k",
     "fp_search", "fp_select", "fp_sparse_attn_fwd", "fp_read_status", "fp_last_error",
-    "fp_abi_version",
+    "fp_abi_version", "fp_flashprefill_noalloc",
 )
+NOALLOC_SCRATCH_BYTES = 80 * 1024 * 1024
 
 
 class FpProblem(ctypes.Structure):
@@ -88,6 +89,7 @@ def load(path: Path = LIB_PATH) -> ctypes.CDLL:
     lib.fp_workspace_bytes.restype = ctypes.c_size_t
     for name in ("fp_flashprefill", "fp_plan", "fp_pool_k", "fp_sparse_attn_fwd"):
         getattr(lib, name).argtypes = [P, vp, vp]
+    lib.fp_flashprefill_noalloc.argtypes = [P, vp]
     lib.fp_search.argtypes = [P, vp, vp, vp, vp]
     lib.fp_select.argtypes = [P, vp, vp, vp, vp]
     lib.fp_read_status.argtypes = [P, vp, vp, ctypes.POINTER(ctypes.c_uint32)]

@@ -8,6 +8,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 
 #include "fp_internal.h"
@@ -238,6 +239,41 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
 
 }  // namespace
 
+// Static device scratch of the allocation-free entry point: the workspace of
+// fp_flashprefill_noalloc (every region of fp_ws_layout) lives in this array,
+// one copy per GPU, held until the process ends. Host code never uses the
+// array's name as an address: the device address of each GPU's copy is read
+// once per device with hipGetSymbolAddress (with that device current) and
+// kept in g_scratch_ptr. Nothing in the workspace has to start at zero (the
+// plan kernel writes every table and counter the later kernels read), so the
+// scratch is never cleared; calls that overlap on one GPU share it and race.
+static __device__ __align__(256) unsigned char scratch[FP_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_on_current_device(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(FP_E_UNSUPPORTED, "device index %d", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!ptr) return fail(FP_E_LAUNCH, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return FP_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int fp_abi_version(void) { return 3; }
@@ -298,6 +334,24 @@ int fp_flashprefill(const fp_problem* p, void* ws, void* stream) {
   fp_ws_layout L;
   int rc = prepare(p, ws, &L);
   if (rc != FP_OK) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if ((rc = run_plan(p, L, ws, s)) != FP_OK) return rc;
+  if ((rc = run_pool(p, L, ws, s)) != FP_OK) return rc;
+  if ((rc = run_search(p, L, ws, nullptr, nullptr, nullptr, nullptr, s)) != FP_OK) return rc;
+  return run_attn(p, L, ws, s);
+}
+
+int fp_flashprefill_noalloc(const fp_problem* p, void* stream) {
+  fp_ws_layout L;
+  int rc = layout(p, &L);
+  if (rc != FP_OK) return rc;
+  if (L.total_bytes > FP_NOALLOC_SCRATCH_BYTES)
+    return fail(FP_E_INVALID_ARG,
+                "problem needs %zu bytes of workspace; the static scratch of "
+                "fp_flashprefill_noalloc holds %zu (use fp_flashprefill with a workspace)",
+                L.total_bytes, static_cast<size_t>(FP_NOALLOC_SCRATCH_BYTES));
+  void* ws = nullptr;
+  if ((rc = scratch_on_current_device(&ws)) != FP_OK) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if ((rc = run_plan(p, L, ws, s)) != FP_OK) return rc;
   if ((rc = run_pool(p, L, ws, s)) != FP_OK) return rc;

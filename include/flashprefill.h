@@ -136,6 +136,21 @@ int fp_select(const fp_problem* p, void* workspace, const float* p_scores,
               const float* m_scores, void* stream);
 int fp_sparse_attn_fwd(const fp_problem* p, void* workspace, void* stream);
 
+/* Allocation-free whole operator. No counterpart in the reference: it is
+ * for callers that cannot allocate device memory or pass a workspace (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same computation and output as fp_flashprefill, but the
+ * workspace is a static device array of FP_NOALLOC_SCRATCH_BYTES per GPU
+ * (held until the process ends); problems whose fp_workspace_bytes() exceed
+ * it are rejected with FP_E_INVALID_ARG before any launch. Calls on one GPU
+ * share that array: calls that overlap on one GPU (other streams, other
+ * threads) race, so a caller serialises them. Status flags land in the
+ * static array and are not readable through fp_read_status. Calls no
+ * hipMalloc / hipFree; the first call on a device reads the array's device
+ * address once (hipGetSymbolAddress). */
+#define FP_NOALLOC_SCRATCH_BYTES (80u * 1024u * 1024u)
+int fp_flashprefill_noalloc(const fp_problem* p, void* stream);
+
 /* Copy the device status word to the host (synchronises `stream`). */
 int fp_read_status(const fp_problem* p, void* workspace, void* stream, uint32_t* status);
 
