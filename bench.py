@@ -34,14 +34,17 @@ def parse():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3,
-                    help="3 (default): the bench line; 2, 4 or 5: a report line for "
-                         "config 2 (Llama shapes at 4K/16K/32K), 4 (Qwen2.5 varlen ragged) or "
-                         "5 (64K decoder-layer attention block)")
+                    help="3 (default): the bench line (with configs 1, 2, 4 and 5 as "
+                         "sub-reports); 1, 2, 4 or 5: that config's report line alone (1: CPU "
+                         "oracle at 4K fp32, 2: Llama shapes at 4K/16K/32K, 4: Qwen2.5 varlen "
+                         "ragged, 5: 64K decoder-layer attention block)")
     ap.add_argument("--seq-len", type=int, default=131072)
     ap.add_argument("--seed", type=int, default=128)
     ap.add_argument("--alpha", type=float, default=0.18)
     ap.add_argument("--no-dense", action="store_true", help="skip the dense baselines")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="leave out the configs 1, 2, 4 and 5 sub-reports of the bench line")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="time budget of the CPU baseline sample")
     ap.add_argument("--collect-traffic", action="store_true",
@@ -272,7 +275,7 @@ def cpu_baseline(q, k, v, alpha, budget_s):
     ``value``)."""
     import torch
     from oracle import flashprefill_oracle as O
-    torch.set_num_threads(os.cpu_count() or 1)
+    torch.set_num_threads(cpu_threads())
     S, Hq, d = q.shape
     nb = (S + 127) // 128
     qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
@@ -302,24 +305,39 @@ def cpu_baseline(q, k, v, alpha, budget_s):
     }
 
 
-def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines):
-    """Time one operator configuration: full call, search stage, attention
-    stage (HIP events on the launch stream), density and the dense baselines
-    (this kernel with every causal block selected, torch SDPA flash per
-    sequence with the KV heads expanded)."""
+def median(xs):
+    xs = sorted(xs)
+    return xs[len(xs) // 2]
+
+
+def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines, dense_reps=3):
+    """Time one operator configuration (HIP events on the launch stream):
+    the public entry point flash_prefill_varlen_func (its cached workspace
+    and argument handling included: what a caller pays per call), the same
+    call on a prebuilt descriptor, the plan, search and attention stages,
+    density, and the dense baselines (this kernel with every causal block
+    selected, torch SDPA flash per sequence with the KV heads expanded;
+    each the median of ``dense_reps`` timings)."""
     import torch
+    from flashprefill_amd import flash_prefill_varlen_func
     from flashprefill_amd.runtime import FlashPrefillCall
     T, Hq, d = q.shape
     Hkv = k.shape[1]
     S_max = max(seq_lens)
     o = torch.empty_like(q)
+
+    def public_call():
+        flash_prefill_varlen_func(q, k, v, o, cu, S_max, alpha, 128, 2, 4, 2)
+
     call = FlashPrefillCall(q, k, v, o, cu, S_max, alpha=alpha, attention_sink=2,
                             window_size=4, last_n_block=2)
     for _ in range(warmup):
+        public_call()
         call.run()
     torch.cuda.synchronize()
     print("bench: timing", file=sys.stderr, flush=True)
-    ms_total = timed(call.run, steps)
+    ms_total = timed(public_call, steps)
+    ms_prebuilt = timed(call.run, steps)
 
     # t_search is pool + score + select, the search of the reference's path
     # (its block-table setup is orchestration); the plan kernel, which builds
@@ -357,7 +375,8 @@ def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines):
     exec_tflops = 4.0 * 128 * 128 * d * n_exec / (ms_attn * 1e-3) / 1e12
     dense_flops = sum(dense_causal_flops(s, Hq, d) for s in seq_lens)
     out = {
-        "ms_total": ms_total, "ms_search": ms_search, "ms_attn": ms_attn,
+        "ms_total": ms_total, "ms_total_prebuilt_call": ms_prebuilt,
+        "ms_search": ms_search, "ms_attn": ms_attn,
         "ms_pool": ms_pool, "ms_score": ms_score, "ms_plan": ms_plan,
         "search_share": ms_search / ms_total,
         "search_share_incl_plan": (ms_search + ms_plan) / ms_total, "executed_blocks": n_exec,
@@ -381,7 +400,7 @@ def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines):
                              window_size=4, last_n_block=2)
     dcall.plan(); dcall.pool(); dcall.search()
     dcall.attn()
-    dense["own_all_blocks_attn_ms"] = timed(dcall.attn, 1)
+    dense["own_all_blocks_attn_ms"] = median([timed(dcall.attn, 1) for _ in range(dense_reps)])
     dense["own_all_blocks_tflops"] = dense_flops / (dense["own_all_blocks_attn_ms"] * 1e-3) / 1e12
     del o2, dcall
     try:
@@ -402,12 +421,13 @@ def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines):
 
         with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
             sdpa_all()
-            dense["sdpa_flash_ms"] = timed(sdpa_all, 2)
+            dense["sdpa_flash_ms"] = median([timed(sdpa_all, 1) for _ in range(dense_reps)])
         dense["sdpa_flash_tflops"] = dense_flops / (dense["sdpa_flash_ms"] * 1e-3) / 1e12
         del parts
     except Exception as exc:  # the flash backend is the only one that fits long sequences
         dense["sdpa_flash_error"] = f"{type(exc).__name__}: {exc}"[:200]
     cands = [x for x in (dense.get("sdpa_flash_ms"), dense.get("own_all_blocks_attn_ms")) if x]
+    dense["reps"] = dense_reps
     if cands:
         dense["fastest_dense_ms"] = min(cands)
         dense["speedup_vs_dense"] = min(cands) / ms_total
@@ -422,35 +442,83 @@ def _rounded(x):
     return x
 
 
-def other_config(args):
+def cpu_threads():
+    """Host threads for the CPU baseline: the box's CPU share (OMP_NUM_THREADS
+    when set, else os.cpu_count())."""
+    return max(1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+
+
+def config1_report(args):
+    """Config 1 (4096 tokens, 8 q / 2 kv heads, d = 64, fp32, seed 0, sinks
+    and 16 stripe columns): the oracle, i.e. the CPU restatement of the
+    reference's native forward (ops/flashprefill_native_forward.py:405-499),
+    timed in full on the host: median of 5 runs after 1 warm-up."""
+    import torch
+    from flashprefill_amd import synth
+    from oracle import flashprefill_oracle as O
+    torch.set_num_threads(cpu_threads())
+    spec = synth.config1_spec(seed=0)
+    q, k, v, _ = synth.make_inputs(spec)
+    qb, kb, vb = q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0)
+    times = []
+    for rep in range(6):
+        t0 = time.perf_counter()
+        res = O.flash_prefill(qb, kb, vb, 128, 2, 4, args.alpha, 2, 0)
+        if rep:
+            times.append((time.perf_counter() - t0) * 1e3)
+    sel = res.traces[0].sel
+    nb = sel.shape[-1]
+    S, Hq, d = q.shape
+    ms = median(times)
+    return _rounded({
+        "case": "config 1: 4096 tokens, 8 q / 2 kv heads, d 64, fp32, native forward, alpha "
+                f"{args.alpha}", "cpu_ms_median": ms, "cpu_ms_runs": times,
+        "cpu_effective_tflops": dense_causal_flops(S, Hq, d) / (ms * 1e-3) / 1e12,
+        "density": int(sel.sum()) / (Hq * nb * (nb + 1) // 2), "cores": torch.get_num_threads(),
+        "cpu": f"{platform.processor() or platform.machine()}, os.cpu_count()={os.cpu_count()}",
+        "kind": "port (oracle/flashprefill_oracle.py flash_prefill)"})
+
+
+def config_cases(config):
+    from flashprefill_amd import synth
+    if config == 2:
+        return [(synth.llama_spec(S, seed=seed), 0.18, f"{S // 1024}K")
+                for S, seed in ((4096, 4), (16384, 16), (32768, 32))]
+    if config == 4:
+        return [(synth.qwen_varlen_spec(), 0.08,
+                 "ragged {256K, 64K, 17K, 3K, 1K}, Qwen2.5-7B heads")]
+    raise SystemExit(f"--config {config}: 1, 2, 3, 4 or 5")
+
+
+def config_results(config, steps, warmup, dense):
     """Configs 2 (Llama shapes at 4K / 16K / 32K) and 4 (Qwen2.5 varlen
-    ragged batch): one JSON report line, secondary to the config-3 bench line."""
+    ragged batch): one result per case."""
     import torch
     from flashprefill_amd import synth
     dev = torch.device("cuda:0")
     results = []
-    if args.config == 5:
-        print(json.dumps(decoder_layer_report(args)), flush=True)
-        return
-    if args.config == 2:
-        cases = [(synth.llama_spec(S, seed=seed), 0.18, f"{S // 1024}K")
-                 for S, seed in ((4096, 4), (16384, 16), (32768, 32))]
-    elif args.config == 4:
-        cases = [(synth.qwen_varlen_spec(), 0.08,
-                  "ragged {256K, 64K, 17K, 3K, 1K}, Qwen2.5-7B heads")]
-    else:
-        raise SystemExit(f"--config {args.config}: 2, 3, 4 or 5")
-    for spec, alpha, name in cases:
-        print(f"bench: config {args.config} {name}", file=sys.stderr, flush=True)
+    for spec, alpha, name in config_cases(config):
+        print(f"bench: config {config} {name}", file=sys.stderr, flush=True)
         q, k, v, cu = synth.make_inputs(spec, device=dev)
-        r = measure(q, k, v, cu, list(spec.seq_lens), alpha, args.steps, args.warmup,
-                    not args.no_dense)
+        r = measure(q, k, v, cu, list(spec.seq_lens), alpha, steps, warmup, dense)
         r.update({"case": name, "seq_lens": list(spec.seq_lens), "num_q_heads": spec.num_q_heads,
                   "num_kv_heads": spec.num_kv_heads, "head_dim": spec.head_dim, "alpha": alpha,
                   "seed": spec.seed})
         results.append(_rounded(r))
         del q, k, v, cu
         torch.cuda.empty_cache()
+    return results
+
+
+def other_config(args):
+    """One JSON report line for config 1, 2, 4 or 5 alone."""
+    if args.config == 5:
+        print(json.dumps(decoder_layer_report(args)), flush=True)
+        return
+    if args.config == 1:
+        print(json.dumps({"report": "config 1", **config1_report(args)}), flush=True)
+        return
+    results = config_results(args.config, args.steps, args.warmup, not args.no_dense)
     print(json.dumps({"report": f"config {args.config}", "n_gpus": 1, "dtype": "bf16",
                       "data": "synthetic (flashprefill_amd/synth.py)",
                       "attention_kernel": attn_kernel_name(), "results": results}), flush=True)
@@ -500,8 +568,8 @@ def decoder_layer_report(args):
         vh = v.repeat_interleave(Hq // Hkv, dim=1).transpose(0, 1).unsqueeze(0)
         with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
             torch.nn.functional.scaled_dot_product_attention(qh, kh, vh, is_causal=True)
-            ms_dense = timed(lambda: torch.nn.functional.scaled_dot_product_attention(
-                qh, kh, vh, is_causal=True), 2)
+            ms_dense = median([timed(lambda: torch.nn.functional.scaled_dot_product_attention(
+                qh, kh, vh, is_causal=True), 1) for _ in range(3)])
         rep["ms_dense_attention_sdpa_flash"] = ms_dense
         rep["ms_layer_with_dense_attention"] = ms_layer - ms_attn + ms_dense
         rep["layer_speedup_vs_dense"] = rep["ms_layer_with_dense_attention"] / ms_layer
@@ -637,6 +705,22 @@ def main():
         "search_roofline": search_roofline,
         "cpu_baseline": cpu,
     }
+    if not args.no_configs:
+        # the other configs, measured in the same run after the headline
+        # (their inputs are generated after the 128K tensors are freed)
+        del q, k, v, cu
+        torch.cuda.empty_cache()
+        sub_steps, sub_warmup = min(args.steps, 5), min(args.warmup, 2)
+        configs = {}
+        for c in (2, 4):
+            configs[f"config_{c}"] = config_results(c, sub_steps, sub_warmup, not args.no_dense)
+        print("bench: config 5", file=sys.stderr, flush=True)
+        sub = argparse.Namespace(steps=sub_steps, warmup=sub_warmup, no_dense=args.no_dense)
+        configs["config_5"] = decoder_layer_report(sub)
+        if not args.no_cpu:
+            print("bench: config 1 (CPU oracle)", file=sys.stderr, flush=True)
+            configs["config_1"] = config1_report(args)
+        line["configs"] = configs
     print(json.dumps(line), flush=True)
 
 

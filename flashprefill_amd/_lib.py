@@ -29,7 +29,7 @@ ABI_VERSION = 3
 EXPORTS = (
     "fp_workspace_layout", "fp_workspace_bytes", "fp_flashprefill", "fp_plan", "fp_pool_k",
     "fp_search", "fp_select", "fp_sparse_attn_fwd", "fp_read_status", "fp_last_error",
-    "fp_abi_version", "fp_flashprefill_noalloc",
+    "fp_abi_version", "fp_flashprefill_noalloc", "fp_kv_cache_write",
 )
 NOALLOC_SCRATCH_BYTES = 80 * 1024 * 1024
 
@@ -68,6 +68,23 @@ class FpWsLayout(ctypes.Structure):
     ]
 
 
+class FpKvCacheArgs(ctypes.Structure):
+    _fields_ = [
+        ("key", ctypes.c_void_p), ("value", ctypes.c_void_p),
+        ("k_stride_tok", ctypes.c_int64), ("k_stride_head", ctypes.c_int64),
+        ("v_stride_tok", ctypes.c_int64), ("v_stride_head", ctypes.c_int64),
+        ("key_cache", ctypes.c_void_p), ("value_cache", ctypes.c_void_p),
+        ("kc_stride_block", ctypes.c_int64), ("kc_stride_slot", ctypes.c_int64),
+        ("kc_stride_head", ctypes.c_int64),
+        ("vc_stride_block", ctypes.c_int64), ("vc_stride_slot", ctypes.c_int64),
+        ("vc_stride_head", ctypes.c_int64),
+        ("slot_mapping", ctypes.c_void_p),
+        ("num_tokens", ctypes.c_int64), ("num_blocks", ctypes.c_int64),
+        ("block_size", ctypes.c_int32), ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32), ("dtype", ctypes.c_int32),
+    ]
+
+
 _LIB = None
 
 
@@ -90,6 +107,7 @@ def load(path: Path = LIB_PATH) -> ctypes.CDLL:
     for name in ("fp_flashprefill", "fp_plan", "fp_pool_k", "fp_sparse_attn_fwd"):
         getattr(lib, name).argtypes = [P, vp, vp]
     lib.fp_flashprefill_noalloc.argtypes = [P, vp]
+    lib.fp_kv_cache_write.argtypes = [ctypes.POINTER(FpKvCacheArgs), vp]
     lib.fp_search.argtypes = [P, vp, vp, vp, vp]
     lib.fp_select.argtypes = [P, vp, vp, vp, vp]
     lib.fp_read_status.argtypes = [P, vp, vp, ctypes.POINTER(ctypes.c_uint32)]

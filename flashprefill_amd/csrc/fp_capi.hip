@@ -359,6 +359,52 @@ int fp_flashprefill_noalloc(const fp_problem* p, void* stream) {
   return run_attn(p, L, ws, s);
 }
 
+int fp_kv_cache_write(const fp_kv_cache_args* a, void* stream) {
+  if (!a) return fail(FP_E_INVALID_ARG, "kv-cache arguments are NULL");
+  if (a->dtype != FP_DTYPE_BF16 && a->dtype != FP_DTYPE_F16)
+    return fail(FP_E_UNSUPPORTED, "kv-cache dtype %d unsupported (bf16 or fp16 only)", a->dtype);
+  if (a->num_tokens < 0 || a->num_blocks < 0 || a->block_size < 1 || a->num_kv_heads < 1 ||
+      a->head_dim < 8 || a->head_dim % 8)
+    return fail(FP_E_INVALID_ARG, "kv-cache sizes out of range (head_dim must be a multiple of 8)");
+  if (a->num_tokens > 0x7fffffff) return fail(FP_E_INVALID_ARG, "too many tokens");
+  if (a->num_tokens == 0) return FP_OK;
+  if (!a->key || !a->value || !a->key_cache || !a->value_cache || !a->slot_mapping)
+    return fail(FP_E_INVALID_ARG, "kv-cache pointers must be non-NULL");
+  if (!aligned16(a->key) || !aligned16(a->value) || !aligned16(a->key_cache) ||
+      !aligned16(a->value_cache))
+    return fail(FP_E_INVALID_ARG, "key/value and caches must be 16-byte aligned");
+  const int64_t strides[10] = {a->k_stride_tok, a->k_stride_head, a->v_stride_tok, a->v_stride_head,
+                               a->kc_stride_block, a->kc_stride_slot, a->kc_stride_head,
+                               a->vc_stride_block, a->vc_stride_slot, a->vc_stride_head};
+  for (int i = 0; i < 10; ++i)
+    if (strides[i] < 0 || strides[i] % 8)
+      return fail(FP_E_INVALID_ARG, "kv-cache strides must be non-negative multiples of 8 elements");
+  fp::KvCacheArgs k;
+  k.key = a->key;
+  k.value = a->value;
+  k.k_stride_tok = a->k_stride_tok;
+  k.k_stride_head = a->k_stride_head;
+  k.v_stride_tok = a->v_stride_tok;
+  k.v_stride_head = a->v_stride_head;
+  k.key_cache = a->key_cache;
+  k.value_cache = a->value_cache;
+  k.kc_stride_block = a->kc_stride_block;
+  k.kc_stride_slot = a->kc_stride_slot;
+  k.kc_stride_head = a->kc_stride_head;
+  k.vc_stride_block = a->vc_stride_block;
+  k.vc_stride_slot = a->vc_stride_slot;
+  k.vc_stride_head = a->vc_stride_head;
+  k.slot_mapping = a->slot_mapping;
+  k.num_tokens = a->num_tokens;
+  k.num_slots = a->num_blocks * a->block_size;
+  k.block_size = a->block_size;
+  k.num_kv_heads = a->num_kv_heads;
+  k.elem_bytes = 2;
+  k.row_bytes = a->head_dim * 2;
+  const hipError_t e = fp::launch_kv_cache_write(k, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? FP_OK : hip_fail(e, "kv-cache write launch");
+}
+
 int fp_read_status(const fp_problem* p, void* ws, void* stream, uint32_t* status) {
   fp_ws_layout L;
   int rc = prepare(p, ws, &L);

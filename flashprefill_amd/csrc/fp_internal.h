@@ -61,7 +61,25 @@ struct AttnArgs {
   float sm_scale_log2;
 };
 
+struct KvCacheArgs {
+  const void* key;
+  const void* value;
+  int64_t k_stride_tok, k_stride_head, v_stride_tok, v_stride_head;
+  void* key_cache;
+  void* value_cache;
+  int64_t kc_stride_block, kc_stride_slot, kc_stride_head;
+  int64_t vc_stride_block, vc_stride_slot, vc_stride_head;
+  const int64_t* slot_mapping;
+  int64_t num_tokens;
+  int64_t num_slots;  // num_blocks * block_size
+  int32_t block_size;
+  int32_t num_kv_heads;
+  int32_t row_bytes;  // head_dim * elem_bytes
+  int32_t elem_bytes;
+};
+
 hipError_t launch_plan(const PlanArgs& a, hipStream_t s);
+hipError_t launch_kv_cache_write(const KvCacheArgs& a, hipStream_t s);
 hipError_t launch_pool(const PoolArgs& a, int dtype, int head_dim, int64_t grid, hipStream_t s);
 hipError_t launch_search(const SearchArgs& a, int dtype, int head_dim, int64_t grid,
                          bool from_scores, hipStream_t s);

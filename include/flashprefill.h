@@ -28,6 +28,8 @@
  *                          ops/flashprefill_native_forward.py:347-403, ops/flashprefill_varlen_func.py:240-409,656
  *   fp_sparse_attn_fwd     _flash_forward / _flash_block_sparse_varlen
  *                          ops/flashprefill_native_forward.py:227-344, ops/flashprefill_varlen_func.py:449-575
+ *   fp_kv_cache_write      the paged KV-cache write the vLLM patch makes before attention
+ *                          (reshape_and_cache_flash, patches/patch_loader_vllm_0_12_0.py:140-149)
  */
 #ifndef FLASHPREFILL_H
 #define FLASHPREFILL_H
@@ -150,6 +152,31 @@ int fp_sparse_attn_fwd(const fp_problem* p, void* workspace, void* stream);
  * address once (hipGetSymbolAddress). */
 #define FP_NOALLOC_SCRATCH_BYTES (80u * 1024u * 1024u)
 int fp_flashprefill_noalloc(const fp_problem* p, void* stream);
+
+/* Paged KV-cache write of the vLLM backend hook: for every token t < num_tokens
+ * with 0 <= slot = slot_mapping[t] < num_blocks * block_size, copy key[t] and
+ * value[t] (num_kv_heads x head_dim each) to key_cache / value_cache at block
+ * slot / block_size, offset slot % block_size. Negative slots (padding) are
+ * skipped, as in vLLM; so are slots past the cache. Strides in elements, head
+ * dim contiguous; rows 16-byte aligned. */
+typedef struct fp_kv_cache_args {
+    const void* key;          /* (tokens, num_kv_heads, head_dim) */
+    const void* value;
+    int64_t k_stride_tok, k_stride_head;
+    int64_t v_stride_tok, v_stride_head;
+    void* key_cache;          /* (num_blocks, block_size, num_kv_heads, head_dim) */
+    void* value_cache;
+    int64_t kc_stride_block, kc_stride_slot, kc_stride_head;
+    int64_t vc_stride_block, vc_stride_slot, vc_stride_head;
+    const int64_t* slot_mapping; /* device, num_tokens entries */
+    int64_t num_tokens;
+    int64_t num_blocks;
+    int32_t block_size;       /* tokens per cache block */
+    int32_t num_kv_heads;
+    int32_t head_dim;         /* a multiple of 8 */
+    int32_t dtype;            /* FP_DTYPE_BF16 or FP_DTYPE_F16 */
+} fp_kv_cache_args;
+int fp_kv_cache_write(const fp_kv_cache_args* a, void* stream);
 
 /* Copy the device status word to the host (synchronises `stream`). */
 int fp_read_status(const fp_problem* p, void* workspace, void* stream, uint32_t* status);
