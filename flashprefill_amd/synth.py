@@ -97,11 +97,14 @@ def _unit(g: torch.Generator, n: int, d: int, device) -> torch.Tensor:
 
 
 def _seq_structure(g: torch.Generator, spec: SynthSpec, S: int,
-                   q: torch.Tensor, k: torch.Tensor, device) -> None:
+                   q: torch.Tensor, k: torch.Tensor, device, meta: Optional[dict] = None) -> None:
     """Add the structured terms to one sequence's q (S,Hq,d), k (S,Hkv,d) in place.
 
     A shared direction with amplitude ``a`` on both a query and a key adds
-    ``a*a/sqrt(d)`` to their logit, so ``a = sqrt(logit * sqrt(d))``.
+    ``a*a/sqrt(d)`` to their logit, so ``a = sqrt(logit * sqrt(d))``. When
+    ``meta`` is given, the planted positions are recorded in it: "stripes"
+    (first token of each stripe run) and "hot" ((head, q-block, k-block)
+    triples); the random draws are the same either way.
     """
     Hq, Hkv, d = spec.num_q_heads, spec.num_kv_heads, spec.head_dim
     G = Hq // Hkv
@@ -128,6 +131,8 @@ def _seq_structure(g: torch.Generator, spec: SynthSpec, S: int,
         u = _unit(g, Hkv, d, device)
         a = amp(spec.stripe_logit)
         starts = torch.randint(spec.block, S, (spec.n_stripes,), generator=g, device=device)
+        if meta is not None:
+            meta["stripes"] = starts.tolist()
         for s0 in starts.tolist():
             s1 = min(S, s0 + spec.stripe_width)
             k[s0:s1] = a * u.unsqueeze(0) + 0.25 * k[s0:s1]
@@ -162,16 +167,19 @@ def _seq_structure(g: torch.Generator, spec: SynthSpec, S: int,
             for _ in range(spec.hot_blocks):
                 qb = int(torch.randint(5, nb, (1,), generator=g, device=device).item())
                 kb = int(torch.randint(0, qb - 4, (1,), generator=g, device=device).item())
+                if meta is not None:
+                    meta.setdefault("hot", []).append((h, qb, kb))
                 q0, q1 = qb * spec.block, min(S, (qb + 1) * spec.block)
                 k0, k1 = kb * spec.block, min(S, (kb + 1) * spec.block)
                 q[q0:q1, h] += a * w[h]
                 k[k0:k1, h // G] += a * w[h]
 
 
-def make_inputs(spec: SynthSpec, device="cpu") -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor,
-                                                        torch.Tensor]:
+def make_inputs(spec: SynthSpec, device="cpu", metas: Optional[List[dict]] = None
+                ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     """Return packed q (T,Hq,d), k (T,Hkv,d), v (T,Hkv,d) in spec.dtype and
-    cu_seqlens (B+1,) int32 on ``device``."""
+    cu_seqlens (B+1,) int32 on ``device``. With ``metas`` (a list), one dict
+    per sequence of the planted positions is appended to it."""
     device = torch.device(device)
     Hq, Hkv, d = spec.num_q_heads, spec.num_kv_heads, spec.head_dim
     assert Hq % Hkv == 0
@@ -184,7 +192,10 @@ def make_inputs(spec: SynthSpec, device="cpu") -> Tuple[torch.Tensor, torch.Tens
         q = torch.randn(S, Hq, d, generator=g, device=device) * base
         k = torch.randn(S, Hkv, d, generator=g, device=device) * base
         v = torch.randn(S, Hkv, d, generator=g, device=device) * base
-        _seq_structure(g, spec, S, q, k, device)
+        meta = {"stripes": [], "hot": []} if metas is not None else None
+        _seq_structure(g, spec, S, q, k, device, meta)
+        if metas is not None:
+            metas.append(meta)
         qs.append(q.to(spec.dtype))
         ks.append(k.to(spec.dtype))
         vs.append(v.to(spec.dtype))
