@@ -53,25 +53,29 @@ struct AttnState {
 // completes behind the softmax, which reads no LDS, instead of stalling the
 // next block (scalar loads share the LDS wait counter, so the compiler waits
 // for them at the first LDS read after them).
-template <typename T, int D, bool DIAG>
+template <typename T, int D, int BLK, bool DIAG>
 __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T::vec8* qb,
                                            const uint4* sk, uint4* sk_w, const uint16_t* sv16,
                                            uint4* sv_w, const uint16_t* kbase,
                                            const uint16_t* vbase, int64_t kst, int64_t vst,
-                                           const TileLanes<D>& tk, const TileLanes<D>& tv,
+                                           const TileLanes<D, BLK, BLK / 32>& tk,
+                                           const TileLanes<D, BLK, BLK / 32>& tv,
                                            int jn, const int32_t* pf, int& jpf, int L, float c,
                                            int w, int lane) {
   constexpr int CH = D / 8;
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
+  constexpr int KT = BLK / 32;  // 32-key tiles of S^T per block
+  constexpr int NW = BLK / 32;  // waves of the workgroup
+  constexpr int NI = TileLanes<D, BLK, NW>::NI;
   const int half = lane >> 5, l32 = lane & 31;
   const int qrow = 32 * w + l32;
 
   // entered with K of this block landed in every wave's part and the barrier
   // passed (V may still be in flight)
-  f32x16 s[4];
+  f32x16 s[KT];
 #pragma unroll
-  for (int t4 = 0; t4 < 4; ++t4) {
+  for (int t4 = 0; t4 < KT; ++t4) {
     s[t4] = f32x16{};
     const int r = 32 * t4 + l32;
 #pragma unroll
@@ -81,12 +85,12 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
     }
   }
   lds_barrier();  // every wave is done with the K buffer
-  if (jn >= 0) issue_tile<D>(sk_w, kbase, kst, tk, jn, L, w, lane);
+  if (jn >= 0) issue_tile<D, BLK, NW>(sk_w, kbase, kst, tk, jn, L, w, lane);
   jpf = sld(pf);
 
   if constexpr (DIAG) {  // key > query is masked on the diagonal block
 #pragma unroll
-    for (int t4 = 0; t4 < 4; ++t4)
+    for (int t4 = 0; t4 < KT; ++t4)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int key = 32 * t4 + 8 * (v >> 2) + 4 * half + (v & 3);
@@ -95,7 +99,7 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
   }
   float mx = -INFINITY;
 #pragma unroll
-  for (int t4 = 0; t4 < 4; ++t4)
+  for (int t4 = 0; t4 < KT; ++t4)
 #pragma unroll
     for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[t4][v]);
   const float m_tile = pair32_max(mx) * c;
@@ -114,10 +118,10 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
   }
   // P rounded to the input type, packed as the B operands of P.V; l adds the
   // rounded P that P.V consumes
-  uint32_t pk[4][8];
+  uint32_t pk[KT][8];
   float psum[2] = {0.0f, 0.0f};
 #pragma unroll
-  for (int t4 = 0; t4 < 4; ++t4)
+  for (int t4 = 0; t4 < KT; ++t4)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float p0 = __builtin_amdgcn_exp2f(fmaf(s[t4][2 * e], c, -st.m_run));
@@ -127,8 +131,8 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
     }
   st.l_part += psum[0] + psum[1];
 
-  if (jn >= 0) vm_barrier<CH / 2>(); else vm_barrier<0>();  // V of this block has landed
-  // O^T += V^T . P^T over 8 steps of 16 keys. B element e of lane (q, half)
+  if (jn >= 0) vm_barrier<NI>(); else vm_barrier<0>();  // V of this block has landed
+  // O^T += V^T . P^T over BLK / 16 steps of 16 keys. B element e of lane (q, half)
   // is key 16 u + (e < 4 ? 4 half + e : 8 + 4 half + e - 4); the A operand
   // (V^T) is read in the same key order with two transposing reads.
   const int g16 = lane >> 4, i16 = lane & 15;
@@ -139,7 +143,7 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
   // faster; the same around S, or around the softmax instead, was not)
   __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
+  for (int u = 0; u < BLK / 16; ++u) {
     const int t4 = u >> 1, hh = u & 1;
     const uint4 pu = make_uint4(pk[t4][4 * hh], pk[t4][4 * hh + 1], pk[t4][4 * hh + 2],
                                 pk[t4][4 * hh + 3]);
@@ -163,17 +167,22 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
     // and every wave's part of the next block's K (the only load in flight)
     // has landed, so the next block starts right after the V refill
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    issue_tile<D>(sv_w, vbase, vst, tv, jn, L, w, lane);
+    issue_tile<D, BLK, NW>(sv_w, vbase, vst, tv, jn, L, w, lane);
   }
 }
 
-template <typename T, int D>
-__global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
+// BLK = 128: 4 waves, 64 KB of LDS (d = 128), two workgroups per CU;
+// BLK = 64: 2 waves, 32 KB, four workgroups per CU. Either way two waves per
+// SIMD (the second launch bound is waves per execution unit), i.e. at most
+// 256 registers per wave.
+template <typename T, int D, int BLK>
+__global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
   constexpr int CH = D / 8;   // 16-byte chunks per row
   constexpr int KS = D / 16;  // MFMA k-steps over the head dim
   constexpr int DT = D / 32;  // 32-row tiles of O^T
-  __shared__ uint4 sk[kBlock * CH];
-  __shared__ uint4 sv[kBlock * CH];
+  constexpr int NW = BLK / 32;
+  __shared__ uint4 sk[BLK * CH];
+  __shared__ uint4 sv[BLK * CH];
 
   int item, h;
   map_item(blockIdx.x, a.Hq, item, h);
@@ -195,7 +204,7 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // wave index, kept in an SGPR
   const int half = lane >> 5, l32 = lane & 31;
   const int qrow = 32 * w + l32;           // query row inside the block
-  const int qg = i * kBlock + qrow;         // query position inside the sequence
+  const int qg = i * BLK + qrow;            // query position inside the sequence
   const bool qvalid = qg < L;
   const float c = a.sm_scale_log2;
 
@@ -203,13 +212,13 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
   const uint16_t* vbase = a.v + t0 * a.vst + static_cast<int64_t>(kvh) * a.vhs;
 
   auto list_at = [&](int n) { return min(max(sld(list + n), 0), i); };
-  TileLanes<D> tk, tv;
+  TileLanes<D, BLK, NW> tk, tv;
   tk.init(a.kst, w, lane);
   tv.init(a.vst, w, lane);
   if (ncnt > 0) {
     const int j0 = list_at(0);
-    issue_tile<D>(sk, kbase, a.kst, tk, j0, L, w, lane);
-    issue_tile<D>(sv, vbase, a.vst, tv, j0, L, w, lane);
+    issue_tile<D, BLK, NW>(sk, kbase, a.kst, tk, j0, L, w, lane);
+    issue_tile<D, BLK, NW>(sv, vbase, a.vst, tv, j0, L, w, lane);
   }
   // Q^T as MFMA B operand (lane: query l32, dims 16 s + 8 half .. +7), loaded
   // after the first block's tile loads and waited for here, so one memory
@@ -246,12 +255,12 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
   int jraw = ncnt > 1 ? sld(list + 1) : 0;
   for (int n = 0; n < nplain; ++n) {
     const int jn = n + 1 < ncnt ? min(max(jraw, 0), i) : -1;
-    attn_block<T, D, false>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv, jn,
+    attn_block<T, D, BLK, false>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv, jn,
                             list + min(n + 2, ncnt - 1), jraw, L, c, w, lane);
   }
   if (has_diag) {
     int unused;
-    attn_block<T, D, true>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv, -1,
+    attn_block<T, D, BLK, true>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv, -1,
                            list, unused, L, c, w, lane);
   }
 
@@ -272,17 +281,22 @@ __global__ __launch_bounds__(256, 2) void k_attn(AttnArgs a) {
   }
 }
 
-hipError_t launch_attn(const AttnArgs& a, int dtype, int head_dim, int64_t grid, hipStream_t s) {
-  if (grid <= 0) return hipSuccess;
-  const dim3 g(static_cast<unsigned>(grid)), blk(256);
-  if (dtype == FP_DTYPE_BF16) {
-    if (head_dim == 128) hipLaunchKernelGGL((k_attn<BF16, 128>), g, blk, 0, s, a);
-    else hipLaunchKernelGGL((k_attn<BF16, 64>), g, blk, 0, s, a);
-  } else {
-    if (head_dim == 128) hipLaunchKernelGGL((k_attn<F16, 128>), g, blk, 0, s, a);
-    else hipLaunchKernelGGL((k_attn<F16, 64>), g, blk, 0, s, a);
-  }
+template <typename T, int D>
+hipError_t launch_attn_t(const AttnArgs& a, int block, int64_t grid, hipStream_t s) {
+  const dim3 g(static_cast<unsigned>(grid));
+  if (block == 128) hipLaunchKernelGGL((k_attn<T, D, 128>), g, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((k_attn<T, D, 64>), g, dim3(128), 0, s, a);
   return hipGetLastError();
+}
+
+hipError_t launch_attn(const AttnArgs& a, int dtype, int head_dim, int block, int64_t grid,
+                       hipStream_t s) {
+  if (grid <= 0) return hipSuccess;
+  if (dtype == FP_DTYPE_BF16)
+    return head_dim == 128 ? launch_attn_t<BF16, 128>(a, block, grid, s)
+                           : launch_attn_t<BF16, 64>(a, block, grid, s);
+  return head_dim == 128 ? launch_attn_t<F16, 128>(a, block, grid, s)
+                         : launch_attn_t<F16, 64>(a, block, grid, s);
 }
 
 }  // namespace fp

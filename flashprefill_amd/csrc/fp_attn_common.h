@@ -121,20 +121,22 @@ __device__ __forceinline__ void dma16_sbase_m0(uint32_t lds, uint64_t sbase, uin
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 1\n\tglobal_load_lds_dwordx4 %1, %2"
                :: "s"(lds), "v"(voff), "s"(sbase) : "memory", "m0");
 }
-// Direct-to-LDS loads of one 128 x D tile (block j of a K or V head). Wave w
-// fills the 1 KB LDS slices w*NI .. w*NI+NI-1; in each slice lane l writes
-// physical chunk l % CH of row slice*RPW + l / CH, so it fetches logical
-// chunk (l % CH) ^ swz(row) of that row. Because swz(row) only depends on
-// (l / CH) and on q modulo a small period, the per-lane part of the source
-// address is a 32-bit byte offset from a small precomputed table and the rest
-// is a wave-uniform (scalar) base.
-template <int D>
+// Direct-to-LDS loads of one R x D tile (rows R*j .. R*j+R-1 of a K, V or
+// Q head) by NW waves. Wave w fills the 1 KB LDS slices w*NI .. w*NI+NI-1;
+// in each slice lane l writes physical chunk l % CH of row slice*RPW + l / CH,
+// so it fetches logical chunk (l % CH) ^ swz(row) of that row. Because
+// swz(row) only depends on (l / CH) and on the slice index modulo a small
+// period, the per-lane part of the source address is a 32-bit byte offset
+// from a small precomputed table and the rest is a wave-uniform (scalar)
+// base.
+template <int D, int R, int NW>
 struct TileLanes {
-  static constexpr int CH = D / 8;      // chunks per row
-  static constexpr int RPW = 64 / CH;   // rows per wave instruction
-  static constexpr int NI = CH / 2;     // instructions per wave per tile
-  static constexpr int PER = D == 128 ? 4 : 2;  // period of swz over q
-  uint32_t off[PER];                    // per-lane byte offsets
+  static constexpr int CH = D / 8;            // chunks per row
+  static constexpr int RPW = 64 / CH;         // rows per wave instruction
+  static constexpr int NI = R * CH / 64 / NW; // instructions per wave per tile
+  static constexpr int PER = D == 128 ? 4 : 2;  // period of swz over the slice index
+  static_assert(NI >= 1 && NI % PER == 0, "every wave's first slice must start a swizzle period");
+  uint32_t off[PER];                          // per-lane byte offsets
   __device__ __forceinline__ void init(int64_t stride, int w, int lane) {
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
@@ -145,16 +147,17 @@ struct TileLanes {
   }
 };
 
-template <int D>
+template <int D, int R, int NW>
 __device__ __forceinline__ void issue_tile(uint4* lds, const uint16_t* base, int64_t stride,
-                                           const TileLanes<D>& tl, int j, int L, int w,
+                                           const TileLanes<D, R, NW>& tl, int j, int L, int w,
                                            int lane) {
-  constexpr int CH = TileLanes<D>::CH, RPW = TileLanes<D>::RPW, NI = TileLanes<D>::NI;
-  if ((j + 1) * kBlock <= L) {
+  typedef TileLanes<D, R, NW> TL;
+  constexpr int CH = TL::CH, RPW = TL::RPW, NI = TL::NI;
+  if ((j + 1) * R <= L) {
     // one scalar base and LDS address per tile; the slices' offsets are
     // scalar adds, so each load costs an add, the M0 write and one wait state
     uint64_t sb = scalar_addr(reinterpret_cast<const char*>(base) +
-                              static_cast<int64_t>(j * kBlock + w * NI * RPW) * stride * 2);
+                              static_cast<int64_t>(j * R + w * NI * RPW) * stride * 2);
     const uint32_t l0 = lds_addr(lds + w * NI * 64);
     // the base was written by VALU (readfirstlane): five wait states before
     // a VMEM instruction reads it; every later use goes through this asm
@@ -162,14 +165,14 @@ __device__ __forceinline__ void issue_tile(uint4* lds, const uint16_t* base, int
     const uint64_t step = static_cast<uint64_t>(RPW) * static_cast<uint64_t>(stride) * 2;
 #pragma unroll
     for (int q = 0; q < NI; ++q)
-      dma16_sbase_m0(l0 + q * 1024, sb + q * step, tl.off[q % TileLanes<D>::PER]);
+      dma16_sbase_m0(l0 + q * 1024, sb + q * step, tl.off[q % TL::PER]);
   } else {  // partial last block: rows past the end read row L-1 (masked keys, p = 0)
 #pragma unroll
     for (int q = 0; q < NI; ++q) {
       const int slot = w * NI + q;
       const int r = slot * RPW + lane / CH;
       const int c = (lane % CH) ^ swz<D>(r);
-      const int gk = min(j * kBlock + r, L - 1);
+      const int gk = min(j * R + r, L - 1);
       dma16_vaddr(lds + slot * 64, base + static_cast<int64_t>(gk) * stride + 8 * c);
     }
   }

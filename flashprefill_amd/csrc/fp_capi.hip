@@ -43,16 +43,16 @@ int validate(const fp_problem* p) {
     return fail(FP_E_UNSUPPORTED, "dtype %d unsupported (bf16 or fp16 only)", p->dtype);
   if (p->head_dim != 64 && p->head_dim != 128)
     return fail(FP_E_UNSUPPORTED, "head_dim %d unsupported (64 or 128)", p->head_dim);
-  if (p->block_size != fp::kBlock)
-    return fail(FP_E_UNSUPPORTED, "block_size %d unsupported (128)", p->block_size);
+  if (p->block_size != 64 && p->block_size != 128)
+    return fail(FP_E_UNSUPPORTED, "block_size %d unsupported (64 or 128)", p->block_size);
   if (p->num_q_heads < 1 || p->num_kv_heads < 1 || p->num_q_heads % p->num_kv_heads)
     return fail(FP_E_INVALID_ARG, "num_q_heads (%d) must be a positive multiple of num_kv_heads (%d)",
                 p->num_q_heads, p->num_kv_heads);
   if (p->batch < 1 || p->batch > fp::kMaxBatch)
     return fail(FP_E_INVALID_ARG, "batch %d outside [1, %d]", p->batch, fp::kMaxBatch);
-  if (p->max_seq_len < 1 || p->max_seq_len > fp::kMaxBlocks * fp::kBlock)
-    return fail(FP_E_INVALID_ARG, "max_seq_len %d outside [1, %d]", p->max_seq_len,
-                fp::kMaxBlocks * fp::kBlock);
+  if (p->max_seq_len < 1 || p->max_seq_len > fp::kMaxBlocks * p->block_size)
+    return fail(FP_E_INVALID_ARG, "max_seq_len %d outside [1, %d] (%d blocks of %d tokens)",
+                p->max_seq_len, fp::kMaxBlocks * p->block_size, fp::kMaxBlocks, p->block_size);
   if (p->total_tokens < 0) return fail(FP_E_INVALID_ARG, "total_tokens < 0");
   if (!p->cu_seqlens) {
     if (p->uniform_seq_len < 0 || p->uniform_seq_len > p->max_seq_len)
@@ -81,8 +81,9 @@ int layout(const fp_problem* p, fp_ws_layout* L) {
   if (rc != FP_OK) return rc;
   memset(L, 0, sizeof(*L));
   const int64_t B = p->batch;
-  const int64_t nb_max = (p->max_seq_len + fp::kBlock - 1) / fp::kBlock;
-  int64_t cap = (p->total_tokens + (fp::kBlock - 1) * B) / fp::kBlock;
+  const int64_t blk = p->block_size;
+  const int64_t nb_max = (p->max_seq_len + blk - 1) / blk;
+  int64_t cap = (p->total_tokens + (blk - 1) * B) / blk;
   if (cap > B * nb_max) cap = B * nb_max;
   if (cap < 1) cap = 1;
   const int64_t full = cap / nb_max, rem = cap % nb_max;
@@ -149,6 +150,7 @@ int run_plan(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   a.nb_max = L.nb_max;
   a.total_tokens = p->total_tokens;
   a.nb_sum_cap = L.nb_sum_cap;
+  a.block = p->block_size;
   const hipError_t e = fp::launch_plan(a, s);
   return e == hipSuccess ? FP_OK : hip_fail(e, "plan launch");
 }
@@ -162,6 +164,7 @@ int run_pool(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   a.mk = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + L.mk_off);
   a.B = p->batch;
   a.Hkv = p->num_kv_heads;
+  a.block = p->block_size;
   const hipError_t e = fp::launch_pool(a, p->dtype, p->head_dim, L.nb_sum_cap, s);
   return e == hipSuccess ? FP_OK : hip_fail(e, "pool launch");
 }
@@ -201,7 +204,7 @@ int run_search(const fp_problem* p, const fp_ws_layout& L, void* ws, float* dp, 
   a.in_p = in_p;
   a.in_m = in_m;
   const bool from_scores = in_p != nullptr;
-  const hipError_t e = fp::launch_search(a, p->dtype, p->head_dim,
+  const hipError_t e = fp::launch_search(a, p->dtype, p->head_dim, p->block_size,
                                          static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap,
                                          from_scores, s);
   return e == hipSuccess ? FP_OK : hip_fail(e, "search launch");
@@ -232,7 +235,7 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   a.Hq = p->num_q_heads;
   a.Hkv = p->num_kv_heads;
   a.sm_scale_log2 = sm_scale_log2(p->head_dim);
-  const hipError_t e = fp::launch_attn(a, p->dtype, p->head_dim,
+  const hipError_t e = fp::launch_attn(a, p->dtype, p->head_dim, p->block_size,
                                        static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap, s);
   return e == hipSuccess ? FP_OK : hip_fail(e, "attention launch");
 }

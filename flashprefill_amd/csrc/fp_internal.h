@@ -16,6 +16,7 @@ struct PlanArgs {
   int32_t nb_max;
   int64_t total_tokens;
   int64_t nb_sum_cap;  // workspace capacity of sum_b NB_b (items, counts, pooled K)
+  int32_t block;       // tokens per block
 };
 
 struct PoolArgs {
@@ -25,6 +26,7 @@ struct PoolArgs {
   uint16_t* mk;  // (sum NB, Hkv, D)
   int32_t B;
   int32_t Hkv;
+  int32_t block;  // tokens per block
 };
 
 struct SearchArgs {
@@ -81,8 +83,9 @@ struct KvCacheArgs {
 hipError_t launch_plan(const PlanArgs& a, hipStream_t s);
 hipError_t launch_kv_cache_write(const KvCacheArgs& a, hipStream_t s);
 hipError_t launch_pool(const PoolArgs& a, int dtype, int head_dim, int64_t grid, hipStream_t s);
-hipError_t launch_search(const SearchArgs& a, int dtype, int head_dim, int64_t grid,
+hipError_t launch_search(const SearchArgs& a, int dtype, int head_dim, int block, int64_t grid,
                          bool from_scores, hipStream_t s);
-hipError_t launch_attn(const AttnArgs& a, int dtype, int head_dim, int64_t grid, hipStream_t s);
+hipError_t launch_attn(const AttnArgs& a, int dtype, int head_dim, int block, int64_t grid,
+                       hipStream_t s);
 
 }  // namespace fp

@@ -4,7 +4,7 @@
 //             counts, block / triangle prefix sums) and the heaviest-first
 //             work-item list; replaces get_cu_tile_seqlens
 //             (ops/flashprefill_varlen_func.py:8-18) with no host sync.
-//   k_pool  — mean of every 128-token K block over its valid rows
+//   k_pool  — mean of every K block (block_size tokens) over its valid rows
 //             (ops/flashprefill_native_forward.py:21-67,
 //              ops/flashprefill_varlen_func.py:35-85). HBM-bound: each K byte
 //             is read once with 16-byte loads, sums are kept in fp32 and the
@@ -113,7 +113,7 @@ __global__ __launch_bounds__(1024) void k_plan(PlanArgs a) {
       }
       tab.seq_start[b] = start;
       tab.seq_len[b] = static_cast<int32_t>(len);
-      nb = (len + kBlock - 1) / kBlock;
+      nb = (len + a.block - 1) / a.block;
       s_pre[b] = static_cast<int32_t>(nb);
     }
     int64_t chunk_nb;
@@ -215,8 +215,8 @@ __global__ __launch_bounds__(256) void k_pool(PoolArgs a) {
   const int b = find_seq(a.tab.seq_tile, a.B, g);
   const int i = static_cast<int>(g - a.tab.seq_tile[b]);
   const int L = a.tab.seq_len[b];
-  const int64_t t0 = a.tab.seq_start[b] + static_cast<int64_t>(i) * kBlock;
-  const int rows = min(kBlock, L - i * kBlock);
+  const int64_t t0 = a.tab.seq_start[b] + static_cast<int64_t>(i) * a.block;
+  const int rows = min(a.block, L - i * a.block);
   constexpr int CPH = D / 8;                 // 16-byte chunks per head row
   const int C = a.Hkv * CPH;                 // chunks per token row (all kv heads)
   const int t = threadIdx.x;

@@ -193,16 +193,18 @@ __device__ __forceinline__ int qswz(int r) {
 }
 
 // dynamic LDS ahead of p / m: the query block, or select_row's scratch
-template <int D, bool FROM_SCORES>
-constexpr size_t search_q_bytes() { return FROM_SCORES ? kSelectScratch : kBlock * D * 2; }
+template <int D, int BLK, bool FROM_SCORES>
+constexpr size_t search_q_bytes() { return FROM_SCORES ? kSelectScratch : BLK * D * 2; }
 
-template <typename T, int D, bool FROM_SCORES>
+template <typename T, int D, int BLK, bool FROM_SCORES>
 __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
-  // 4 workgroups per CU: 4 x (32 KB query block + 2 x 4 KB p / m at 1024
-  // blocks) = 160 KB of LDS, and at most 128 VGPRs per wave
+  // 4 workgroups per CU at BLK = 128: 4 x (32 KB query block + 2 x 4 KB p / m
+  // at 1024 blocks) = 160 KB of LDS, and at most 128 VGPRs per wave
+  constexpr int RG = BLK / 32;  // 32-row groups of the query block
   extern __shared__ uint4 dyn4[];
   uint4* sq = dyn4;  // the query block (score mode only)
-  float* pl = reinterpret_cast<float*>(reinterpret_cast<char*>(dyn4) + search_q_bytes<D, FROM_SCORES>());
+  float* pl = reinterpret_cast<float*>(reinterpret_cast<char*>(dyn4) +
+                                       search_q_bytes<D, BLK, FROM_SCORES>());
   float* ml = pl + a.nb_max;
   int item, h;
   map_item(blockIdx.x, a.Hq, item, h);
@@ -254,28 +256,28 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
     // reads it as MFMA A operands (rows 32*rg + l32, dims 16*s + 8*half .. +7).
     // The wave's first key tile is loaded in the same wait.
     {
-      TileLanes<D> tq;
+      TileLanes<D, BLK, 4> tq;
       tq.init(a.qst, __builtin_amdgcn_readfirstlane(w), lane);
-      issue_tile<D>(sq, a.q + t0 * a.qst + static_cast<int64_t>(h) * a.qhs, a.qst, tq, i, L,
-                    __builtin_amdgcn_readfirstlane(w), lane);
+      issue_tile<D, BLK, 4>(sq, a.q + t0 * a.qst + static_cast<int64_t>(h) * a.qhs, a.qst, tq,
+                            i, L, __builtin_amdgcn_readfirstlane(w), lane);
       if (w < ntiles) load_kb(w);
       asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-      if ((i + 1) * kBlock > L) {
-        for (int cidx = t; cidx < kBlock * CH; cidx += 256)
-          if (i * kBlock + cidx / CH >= L) sq[cidx] = zero4();
+      if ((i + 1) * BLK > L) {
+        for (int cidx = t; cidx < BLK * CH; cidx += 256)
+          if (i * BLK + cidx / CH >= L) sq[cidx] = zero4();
         __syncthreads();
       }
     }
     for (int tile = w; tile < ntiles; tile += 4) {
       const int j = 32 * tile + l32;
       const bool jv = j < n;
-      f32x16 acc[4];
+      f32x16 acc[RG];
 #pragma unroll
-      for (int rg = 0; rg < 4; ++rg) acc[rg] = f32x16{};
+      for (int rg = 0; rg < RG; ++rg) acc[rg] = f32x16{};
 #pragma unroll
       for (int s = 0; s < KS; ++s)
 #pragma unroll
-        for (int rg = 0; rg < 4; ++rg) {
+        for (int rg = 0; rg < RG; ++rg) {
           const int r = 32 * rg + l32;
           const uint4 qop = sq[r * CH + ((2 * s + half) ^ qswz<D>(r))];
           acc[rg] = T::mfma32(as_vec8<T>(qop), kb[s], acc[rg]);
@@ -291,29 +293,30 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
       // acc[rg][v] = Q[32 rg + 8 (v/4) + 4 half + v%4] . mk[j]
       float mx = -INFINITY, sum = 0.0f, m;
 #pragma unroll
-      for (int rg = 0; rg < 4; ++rg)
+      for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
         for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc[rg][v]);
-      if (tile + 1 < ntiles) {  // every column j < i: all 128 rows count
+      if (tile + 1 < ntiles) {  // every column j < i: all BLK rows count
         m = pair32_max(mx) * c;
 #pragma unroll
-        for (int rg = 0; rg < 4; ++rg)
+        for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
           for (int v = 0; v < 16; ++v) sum += __builtin_amdgcn_exp2f(fmaf(acc[rg][v], c, -m));
       } else {
-        // last tile: j < i all rows, j == i row 127 only (acc[3][15] of the
-        // upper half-wave), j > i none. The case is uniform over a lane's 64
-        // values, so the full-tile reduction runs for every lane and one
-        // select per lane picks the result (the same arithmetic on the rows
-        // that count, no per-element masking)
-        const bool full = j < i, row127 = j == i && half == 1;
-        mx = full ? mx : (row127 ? acc[3][15] : -INFINITY);
+        // last tile: j < i all rows, j == i the last row BLK - 1 only
+        // (acc[RG - 1][15] of the upper half-wave), j > i none. The case is
+        // uniform over a lane's values, so the full-tile reduction runs for
+        // every lane and one select per lane picks the result (the same
+        // arithmetic on the rows that count, no per-element masking)
+        const bool full = j < i, rowlast = j == i && half == 1;
+        mx = full ? mx : (rowlast ? acc[RG - 1][15] : -INFINITY);
         m = pair32_max(mx) * c;
 #pragma unroll
-        for (int rg = 0; rg < 4; ++rg)
+        for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
           for (int v = 0; v < 16; ++v) sum += __builtin_amdgcn_exp2f(fmaf(acc[rg][v], c, -m));
-        sum = full ? sum : (row127 ? __builtin_amdgcn_exp2f(fmaf(acc[3][15], c, -m)) : 0.0f);
+        sum = full ? sum
+                   : (rowlast ? __builtin_amdgcn_exp2f(fmaf(acc[RG - 1][15], c, -m)) : 0.0f);
       }
       sum = pair32_sum(sum);
       if (half == 0 && jv) {
@@ -333,36 +336,39 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
   select_row(pl, ml, n, i, nb, a, list, count, dyn4);
 }
 
-template <typename T, int D, bool FROM_SCORES>
+template <typename T, int D, int BLK, bool FROM_SCORES>
 hipError_t launch_search_t(const SearchArgs& a, int64_t grid, hipStream_t s) {
-  const size_t shm = search_q_bytes<D, FROM_SCORES>() +
+  const size_t shm = search_q_bytes<D, BLK, FROM_SCORES>() +
                      2 * sizeof(float) * static_cast<size_t>(a.nb_max);
   if (shm > 48 * 1024) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_search<T, D, FROM_SCORES>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             static_cast<int>(shm));
+    const hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&k_search<T, D, BLK, FROM_SCORES>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(shm));
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((k_search<T, D, FROM_SCORES>), dim3(static_cast<unsigned>(grid)), dim3(256),
-                     shm, s, a);
+  hipLaunchKernelGGL((k_search<T, D, BLK, FROM_SCORES>), dim3(static_cast<unsigned>(grid)),
+                     dim3(256), shm, s, a);
   return hipGetLastError();
 }
 
-hipError_t launch_search(const SearchArgs& a, int dtype, int head_dim, int64_t grid,
+template <typename T, int D>
+hipError_t launch_search_d(const SearchArgs& a, int block, int64_t grid, bool from_scores,
+                           hipStream_t s) {
+  if (block == 128)
+    return from_scores ? launch_search_t<T, D, 128, true>(a, grid, s)
+                       : launch_search_t<T, D, 128, false>(a, grid, s);
+  return from_scores ? launch_search_t<T, D, 64, true>(a, grid, s)
+                     : launch_search_t<T, D, 64, false>(a, grid, s);
+}
+
+hipError_t launch_search(const SearchArgs& a, int dtype, int head_dim, int block, int64_t grid,
                          bool from_scores, hipStream_t s) {
   if (grid <= 0) return hipSuccess;
-  if (dtype == FP_DTYPE_BF16) {
-    if (head_dim == 128)
-      return from_scores ? launch_search_t<BF16, 128, true>(a, grid, s)
-                         : launch_search_t<BF16, 128, false>(a, grid, s);
-    return from_scores ? launch_search_t<BF16, 64, true>(a, grid, s)
-                       : launch_search_t<BF16, 64, false>(a, grid, s);
-  }
-  if (head_dim == 128)
-    return from_scores ? launch_search_t<F16, 128, true>(a, grid, s)
-                       : launch_search_t<F16, 128, false>(a, grid, s);
-  return from_scores ? launch_search_t<F16, 64, true>(a, grid, s)
-                     : launch_search_t<F16, 64, false>(a, grid, s);
+  if (dtype == FP_DTYPE_BF16)
+    return head_dim == 128 ? launch_search_d<BF16, 128>(a, block, grid, from_scores, s)
+                           : launch_search_d<BF16, 64>(a, block, grid, from_scores, s);
+  return head_dim == 128 ? launch_search_d<F16, 128>(a, block, grid, from_scores, s)
+                         : launch_search_d<F16, 64>(a, block, grid, from_scores, s);
 }
 
 }  // namespace fp

@@ -47,7 +47,7 @@ def seq_slices(cu: Sequence[int]):
 
 def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n=2,
                native=False, check_oracle_scores=True, attention=True,
-               min_budget=0, attn_rows=None) -> StageReport:
+               min_budget=0, attn_rows=None, block=128) -> StageReport:
     """Run plan/pool/search(dump)/select/attn on the GPU and compare each stage
     with the oracle. q/k/v are CPU tensors (T, H, d); cu_list python ints.
     ``attn_rows`` {sequence: [(head, q-block), ...]} restricts the attention
@@ -59,7 +59,7 @@ def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n
     cu = torch.tensor(cu_list, dtype=torch.int32, device=dev)
     call = FlashPrefillCall(qd, kd, vd, od, cu, max_seq_len, alpha=alpha, attention_sink=sink,
                             window_size=window, last_n_block=last_n, native_normalize=native,
-                            min_budget=min_budget)
+                            min_budget=min_budget, block_size=block)
     rep = StageReport()
     call.plan()
     call.pool()
@@ -80,10 +80,10 @@ def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n
             oracle_ps.append(torch.zeros(q.shape[1], 0, 0))
             oracle_ms.append(torch.zeros(q.shape[1], 0, 0))
             continue
-        mk_o = O.pool_k(k[s0:s1])
+        mk_o = O.pool_k(k[s0:s1], block)
         rep.pool_ulp = max(rep.pool_ulp, ulp_diff_16(mk_gpu[tile[b]:tile[b + 1]], mk_o))
         # scores from the GPU's own pooled K (isolates the score kernel)
-        p_o, m_o = O.block_score(q[s0:s1], mk_gpu[tile[b]:tile[b + 1]])
+        p_o, m_o = O.block_score(q[s0:s1], mk_gpu[tile[b]:tile[b + 1]], block)
         nb = p_o.shape[-1]
         tril = torch.tril(torch.ones(nb, nb, dtype=torch.bool)).expand_as(p_o)
         dm = (gm[b][tril] - m_o[tril]).abs() / m_o[tril].abs().clamp_min(1.0)
@@ -96,7 +96,7 @@ def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n
                                      native, alpha, sink, window, last_n, min_budget)
         rep.sel_from_gpu_scores_mismatch += int((sel_g != gpu_sel[b]).sum())
         # end-to-end selection vs the oracle's own scores (tie flips)
-        p_e, m_e = O.block_score(q[s0:s1], mk_o)
+        p_e, m_e = O.block_score(q[s0:s1], mk_o, block)
         sel_e = O.select_from_scores(p_e, m_e, native, alpha, sink, window, last_n, min_budget)
         rep.e2e_flips += int((sel_e != gpu_sel[b]).sum())
         rep.cells += int(tril.sum())
@@ -127,16 +127,17 @@ def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n
         for b, (s0, s1) in enumerate(seq_slices(cu_list)):
             if s1 == s0:
                 continue
+            k_tile = min(block, 128)
             if attn_rows is None:
-                ref = O.sparse_attention(q[s0:s1], k[s0:s1], v[s0:s1], gpu_sel[b])
+                ref = O.sparse_attention(q[s0:s1], k[s0:s1], v[s0:s1], gpu_sel[b], block, k_tile)
                 diffs.append((out[s0:s1].float() - ref.float()).abs().reshape(-1))
                 continue
             sub = torch.zeros_like(gpu_sel[b])
             for h, i in attn_rows.get(b, []):
                 sub[h, i] = gpu_sel[b][h, i]
-            ref = O.sparse_attention(q[s0:s1], k[s0:s1], v[s0:s1], sub)
+            ref = O.sparse_attention(q[s0:s1], k[s0:s1], v[s0:s1], sub, block, k_tile)
             for h, i in attn_rows.get(b, []):
-                r0, r1 = i * 128, min((i + 1) * 128, s1 - s0)
+                r0, r1 = i * block, min((i + 1) * block, s1 - s0)
                 diffs.append((out[s0 + r0:s0 + r1, h].float() - ref[r0:r1, h].float())
                              .abs().reshape(-1))
         d = torch.cat(diffs)

@@ -69,10 +69,26 @@ def test_layout_bounds():
     assert _lib.load().fp_workspace_bytes(ctypes.byref(_problem())) == L.total_bytes
 
 
+def test_layout_bounds_block_64():
+    rc, L = _layout(_problem(block_size=64))
+    assert rc == _lib.FP_OK
+    assert L.nb_max == 64
+    assert L.nb_sum_cap == (6000 + 63 * 3) // 64
+    cap = L.nb_sum_cap
+    assert L.tri_cap == (cap // 64) * 64 * 65 // 2 + (cap % 64) * (cap % 64 + 1) // 2
+    # 8192 blocks per sequence: 524288 tokens at block 64
+    rc, _ = _layout(_problem(block_size=64, max_seq_len=8192 * 64, total_tokens=8192 * 64,
+                             batch=1))
+    assert rc == _lib.FP_OK
+    rc, _ = _layout(_problem(block_size=64, max_seq_len=8192 * 64 + 1, batch=1))
+    assert rc == _lib.FP_E_INVALID_ARG
+
+
 @pytest.mark.parametrize("field,value,code", [
     ("dtype", 7, _lib.FP_E_UNSUPPORTED),
     ("head_dim", 96, _lib.FP_E_UNSUPPORTED),
-    ("block_size", 64, _lib.FP_E_UNSUPPORTED),
+    ("block_size", 256, _lib.FP_E_UNSUPPORTED),
+    ("block_size", 96, _lib.FP_E_UNSUPPORTED),
     ("num_kv_heads", 3, _lib.FP_E_INVALID_ARG),
     ("batch", 0, _lib.FP_E_INVALID_ARG),
     ("max_seq_len", 0, _lib.FP_E_INVALID_ARG),

@@ -205,4 +205,4 @@ def test_error_paths():
                                   q96.clone(), cu, T, 0.1)
     with pytest.raises(NotImplementedError):
         flash_prefill_varlen_func(qb, qb[:, :1].contiguous(), qb[:, :1].contiguous(), qb.clone(),
-                                  cu, T, 0.1, block_size=64)
+                                  cu, T, 0.1, block_size=256)

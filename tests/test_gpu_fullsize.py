@@ -26,14 +26,14 @@ pytestmark = pytest.mark.gpu
 ALPHA = 0.18
 
 
-def _sampled_rows(call, out, b, S, ref, label):
+def _sampled_rows(call, out, b, S, ref, label, block=128):
     """Compare the GPU's lists and output of sequence b with the oracle's
     row pipeline on the rows in ``ref``; returns (flips, rows checked)."""
     tile, tri, start, _ = call.seq_tables()
     t0 = start[b]
     cnt = call.counts().cpu()
     idx = call.index_lists().cpu()
-    nb = (S + 127) // 128
+    nb = (S + block - 1) // block
     flips, checked = 0, 0
     for (h, i), (sel_o, out_o) in ref.items():
         c = int(cnt[h, tile[b] + i])
@@ -46,7 +46,7 @@ def _sampled_rows(call, out, b, S, ref, label):
         flips += row_flips
         if row_flips:
             continue  # the oracle output is for a different block set
-        q0, q1 = t0 + i * 128, t0 + min((i + 1) * 128, S)
+        q0, q1 = t0 + i * block, t0 + min((i + 1) * block, S)
         d = (out[q0:q1, h].float().cpu() - out_o.float()).abs()
         print(f"  {label} row {(h, i)}: {c} blocks, out max {d.max().item():.2e} "
               f"mean {d.mean().item():.2e}", flush=True)
@@ -56,12 +56,12 @@ def _sampled_rows(call, out, b, S, ref, label):
     return flips, checked
 
 
-def _run_twice(q, k, v, cu, max_len, alpha):
+def _run_twice(q, k, v, cu, max_len, alpha, block=128):
     outs = []
     for _ in range(2):
         o = torch.full_like(q, float("nan"))
         call = FlashPrefillCall(q, k, v, o, cu, max_len, alpha=alpha, attention_sink=2,
-                                window_size=4, last_n_block=2)
+                                window_size=4, last_n_block=2, block_size=block)
         call.run()
         torch.cuda.synchronize()
         assert call.status() == 0
@@ -71,12 +71,12 @@ def _run_twice(q, k, v, cu, max_len, alpha):
     return call, outs[0]
 
 
-def _full_case(S, seed, rows, oracle_heads, label, every_row=True, spec=None):
+def _full_case(S, seed, rows, oracle_heads, label, every_row=True, spec=None, block=128):
     spec = spec or synth.llama_spec(S, seed=seed)
     print(f"\n  {label}: S={S} Hq={spec.num_q_heads} Hkv={spec.num_kv_heads} d={spec.head_dim} "
-          f"seed={spec.seed}", flush=True)
+          f"seed={spec.seed} block={block}", flush=True)
     q, k, v, cu = synth.make_inputs(spec, device="cuda:0")
-    call, out = _run_twice(q, k, v, cu, S, ALPHA)
+    call, out = _run_twice(q, k, v, cu, S, ALPHA, block)
     qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
     if every_row:
         n_rows, n_sel = check_every_row_selection(call, qc, kc, native=False, alpha=ALPHA,
@@ -84,8 +84,8 @@ def _full_case(S, seed, rows, oracle_heads, label, every_row=True, spec=None):
         print(f"  {label}: every row's selection matches ({n_rows} cells, {n_sel} selected)",
               flush=True)
     ref = O.flashprefill_rows(qc, kc, vc, rows, alpha=ALPHA, attention_sink=2, window=4,
-                              last_n=2, native=False)
-    flips, checked = _sampled_rows(call, out, 0, S, ref, label)
+                              last_n=2, native=False, block=block)
+    flips, checked = _sampled_rows(call, out, 0, S, ref, label, block)
     print(f"  {label}: threshold flips {flips}, rows checked {checked}/{len(ref)}", flush=True)
     assert flips <= 1
     assert checked >= len(ref) - 1
@@ -94,6 +94,15 @@ def _full_case(S, seed, rows, oracle_heads, label, every_row=True, spec=None):
 def test_128k_every_row_selection_and_sampled_rows():
     rows = [(0, 1023), (5, 1000), (13, 777), (31, 512), (7, 300), (20, 64), (26, 2), (9, 0)]
     _full_case(131072, 128, rows, oracle_heads=[7], label="128K")
+
+
+def test_128k_block_64_sampled_rows():
+    # 64-token blocks at 128K: 2048 blocks per row, 2-wave attention workgroups
+    spec = synth.SynthSpec(seq_lens=(131072,), num_q_heads=32, num_kv_heads=8, head_dim=128,
+                           seed=129, block=64)
+    rows = [(0, 2047), (5, 2000), (13, 1500), (31, 700), (7, 64), (20, 3), (9, 0)]
+    _full_case(131072, 129, rows, oracle_heads=[], label="128K block 64", every_row=False,
+               spec=spec, block=64)
 
 
 def test_256k_sampled_rows():

@@ -115,3 +115,28 @@ def test_zero_length_sequences_in_a_ragged_batch():
     lens = [0, 300, 0, 128, 1, 0, 640, 0]
     q, k, v, cu = _rand_inputs(lens, 8, 2, 128, torch.bfloat16, 3, scale=1.5)
     _check(run_stages(q, k, v, cu, max(lens), alpha=0.18))
+
+
+@pytest.mark.parametrize("native", [False, True])
+def test_block_size_64_ragged(native):
+    # 64-token blocks (the smallest block the reference's tile pruning
+    # admits): 2-wave attention workgroups, 64-row query blocks in the search;
+    # ragged lengths with partial blocks, a 1-token and an empty sequence
+    lens = [300, 64, 1, 0, 640, 129]
+    q, k, v, cu = _rand_inputs(lens, 8, 2, 128, torch.bfloat16, 5, scale=1.5)
+    _check(run_stages(q, k, v, cu, max(lens), alpha=0.18, native=native, block=64))
+
+
+def test_block_size_64_structured_16k_fp16_d64():
+    spec = synth.SynthSpec(seq_lens=(16384,), num_q_heads=8, num_kv_heads=2, head_dim=64,
+                           dtype=torch.float16, seed=64, block=64)
+    q, k, v, cu = synth.make_inputs(spec)
+    nb = 16384 // 64
+    rows = {0: [(0, nb - 1), (3, nb // 2), (7, 17), (5, 0)]}
+    _check(run_stages(q, k, v, cu.tolist(), 16384, alpha=0.12, attn_rows=rows, block=64))
+
+
+def test_block_size_64_min_budget_native():
+    lens = [1000, 777]
+    q, k, v, cu = _rand_inputs(lens, 4, 4, 128, torch.bfloat16, 6, scale=2.0)
+    _check(run_stages(q, k, v, cu, 1000, alpha=0.9, native=True, min_budget=5, block=64))
