@@ -470,7 +470,24 @@ def config1_report(args):
     nb = sel.shape[-1]
     S, Hq, d = q.shape
     ms = median(times)
-    return _rounded({
+    gpu = {}
+    if torch.cuda.is_available():
+        # the same call on the GPU (fp32 kernels), for the GPU / CPU ratio
+        from flashprefill_amd import flash_prefill
+        dev = torch.device("cuda:0")
+        qd, kd, vd = qb.to(dev), kb.to(dev), vb.to(dev)
+        od = torch.empty_like(qd)
+
+        def gpu_call():
+            flash_prefill(qd, kd, vd, od, 128, 2, 4, args.alpha, 2, 0)
+
+        gpu_call()
+        gpu_ms = timed(gpu_call, 20)
+        err = (od[0].cpu() - res.out[0]).abs()
+        gpu = {"gpu_ms": gpu_ms, "gpu_effective_tflops": dense_causal_flops(S, Hq, d) /
+               (gpu_ms * 1e-3) / 1e12, "gpu_speedup_vs_cpu": ms / gpu_ms,
+               "gpu_vs_cpu_max_abs_diff": f"{float(err.max()):.3e}", "gpu_dtype": "fp32"}
+    return _rounded({**gpu,
         "case": "config 1: 4096 tokens, 8 q / 2 kv heads, d 64, fp32, native forward, alpha "
                 f"{args.alpha}", "cpu_ms_median": ms, "cpu_ms_runs": times,
         "cpu_effective_tflops": dense_causal_flops(S, Hq, d) / (ms * 1e-3) / 1e12,

@@ -22,6 +22,7 @@ FP_E_UNSUPPORTED = -2
 FP_E_LAUNCH = -3
 FP_DTYPE_BF16 = 0
 FP_DTYPE_F16 = 1
+FP_DTYPE_F32 = 2
 FP_STATUS_SEQ_TOO_LONG = 1
 FP_STATUS_BAD_CU_SEQLENS = 2
 ABI_VERSION = 3

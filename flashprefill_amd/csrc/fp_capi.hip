@@ -36,11 +36,13 @@ size_t align_up(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+int64_t elem_bytes(int dtype) { return dtype == FP_DTYPE_F32 ? 4 : 2; }
+
 int validate(const fp_problem* p) {
   if (!p) return fail(FP_E_INVALID_ARG, "problem descriptor is NULL");
   if (!p->q || !p->k || !p->v || !p->o) return fail(FP_E_INVALID_ARG, "q/k/v/o must be non-NULL");
-  if (p->dtype != FP_DTYPE_BF16 && p->dtype != FP_DTYPE_F16)
-    return fail(FP_E_UNSUPPORTED, "dtype %d unsupported (bf16 or fp16 only)", p->dtype);
+  if (p->dtype != FP_DTYPE_BF16 && p->dtype != FP_DTYPE_F16 && p->dtype != FP_DTYPE_F32)
+    return fail(FP_E_UNSUPPORTED, "dtype %d unsupported (bf16, fp16 or fp32)", p->dtype);
   if (p->head_dim != 64 && p->head_dim != 128)
     return fail(FP_E_UNSUPPORTED, "head_dim %d unsupported (64 or 128)", p->head_dim);
   if (p->block_size != 64 && p->block_size != 128)
@@ -64,9 +66,11 @@ int validate(const fp_problem* p) {
     return fail(FP_E_INVALID_ARG, "q/k/v/o must be 16-byte aligned");
   const int64_t strides[8] = {p->q_stride_tok, p->q_stride_head, p->k_stride_tok, p->k_stride_head,
                               p->v_stride_tok, p->v_stride_head, p->o_stride_tok, p->o_stride_head};
+  const int64_t vec = 16 / elem_bytes(p->dtype);  // elements per 16 bytes
   for (int s = 0; s < 8; ++s)
-    if (strides[s] < 0 || strides[s] % 8)
-      return fail(FP_E_INVALID_ARG, "strides must be non-negative multiples of 8 elements");
+    if (strides[s] < 0 || strides[s] % vec)
+      return fail(FP_E_INVALID_ARG, "strides must be non-negative multiples of 16 bytes "
+                                    "(%lld elements)", static_cast<long long>(vec));
   for (int s = 0; s < 8; ++s)
     if (strides[s] >= (int64_t(1) << 24))
       return fail(FP_E_UNSUPPORTED, "strides of 2^24 elements or more are not supported");
@@ -96,7 +100,8 @@ int layout(const fp_problem* p, fp_ws_layout* L) {
   if (Hq * tri >= (int64_t(1) << 31))
     return fail(FP_E_UNSUPPORTED, "index lists of 2^31 entries or more are not supported");
   // the search addresses a sequence's pooled keys with 32-bit byte offsets
-  if (nb_max * Hkv * d * 2 >= (int64_t(1) << 31))
+  const int64_t eb = elem_bytes(p->dtype);
+  if (nb_max * Hkv * d * eb >= (int64_t(1) << 31))
     return fail(FP_E_UNSUPPORTED, "pooled keys of 2^31 bytes or more per sequence are not supported");
   size_t off = 0;
   L->status_off = off;     off = align_up(off + 4);
@@ -105,7 +110,7 @@ int layout(const fp_problem* p, fp_ws_layout* L) {
   L->seq_start_off = off;  off = align_up(off + 8 * B);
   L->seq_len_off = off;    off = align_up(off + 4 * B);
   L->items_off = off;      off = align_up(off + sizeof(fp::ItemRec) * cap);
-  L->mk_off = off;         off = align_up(off + 2 * cap * Hkv * d);
+  L->mk_off = off;         off = align_up(off + eb * cap * Hkv * d);
   L->cnt_off = off;        off = align_up(off + 4 * Hq * cap);
   L->idx_off = off;        off = align_up(off + 4 * Hq * tri);
   L->total_bytes = off;
@@ -235,8 +240,11 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   a.Hq = p->num_q_heads;
   a.Hkv = p->num_kv_heads;
   a.sm_scale_log2 = sm_scale_log2(p->head_dim);
-  const hipError_t e = fp::launch_attn(a, p->dtype, p->head_dim, p->block_size,
-                                       static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap, s);
+  const int64_t grid = static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap;
+  const hipError_t e =
+      p->dtype == FP_DTYPE_F32
+          ? fp::launch_attn_f32(a, p->head_dim, p->block_size, grid, s)
+          : fp::launch_attn(a, p->dtype, p->head_dim, p->block_size, grid, s);
   return e == hipSuccess ? FP_OK : hip_fail(e, "attention launch");
 }
 

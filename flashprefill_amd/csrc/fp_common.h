@@ -115,6 +115,16 @@ __device__ __forceinline__ void map_item(int w, int num_q_heads, int& item, int&
   }
 }
 
+// Sequence owning global block g (binary search over seq_tile).
+__device__ __forceinline__ int find_seq(const int64_t* seq_tile, int B, int64_t g) {
+  int lo = 0, hi = B - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (seq_tile[mid] <= g) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
 // One work item as the plan kernel records it (32 bytes, read with one scalar
 // load by the persistent attention kernel).
 struct ItemRec {

@@ -87,5 +87,7 @@ hipError_t launch_search(const SearchArgs& a, int dtype, int head_dim, int block
                          bool from_scores, hipStream_t s);
 hipError_t launch_attn(const AttnArgs& a, int dtype, int head_dim, int block, int64_t grid,
                        hipStream_t s);
+hipError_t launch_attn_f32(const AttnArgs& a, int head_dim, int block, int64_t grid,
+                           hipStream_t s);
 
 }  // namespace fp

@@ -196,16 +196,6 @@ __global__ __launch_bounds__(1024) void k_plan(PlanArgs a) {
   if (t == 0) *tab.status = s_status;
 }
 
-// Sequence owning global block g (binary search over seq_tile).
-__device__ __forceinline__ int find_seq(const int64_t* seq_tile, int B, int64_t g) {
-  int lo = 0, hi = B - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (seq_tile[mid] <= g) lo = mid; else hi = mid - 1;
-  }
-  return lo;
-}
-
 template <typename T, int D>
 __global__ __launch_bounds__(256) void k_pool(PoolArgs a) {
   __shared__ float red[256 * 8];
@@ -271,6 +261,29 @@ __global__ __launch_bounds__(256) void k_pool(PoolArgs a) {
   }
 }
 
+// fp32 keys: the block mean summed in fp64 (in row order) and rounded once to
+// fp32, one thread per (kv head, dim) element of the block (consecutive
+// threads read consecutive addresses of a row).
+__global__ __launch_bounds__(256) void k_pool_f32(PoolArgs a, int head_dim) {
+  const int64_t g = blockIdx.x;
+  const int64_t nsum = a.tab.seq_tile[a.B];
+  if (g >= nsum) return;
+  const int b = find_seq(a.tab.seq_tile, a.B, g);
+  const int i = static_cast<int>(g - a.tab.seq_tile[b]);
+  const int L = a.tab.seq_len[b];
+  const int64_t t0 = a.tab.seq_start[b] + static_cast<int64_t>(i) * a.block;
+  const int rows = min(a.block, L - i * a.block);
+  const float* k = reinterpret_cast<const float*>(a.k);
+  float* out = reinterpret_cast<float*>(a.mk) + g * static_cast<int64_t>(a.Hkv) * head_dim;
+  for (int e = threadIdx.x; e < a.Hkv * head_dim; e += blockDim.x) {
+    const int hh = e / head_dim, x = e % head_dim;
+    const float* src = k + t0 * a.kst + hh * a.khs + x;
+    double sum = 0.0;
+    for (int r = 0; r < rows; ++r) sum += static_cast<double>(src[static_cast<int64_t>(r) * a.kst]);
+    out[e] = static_cast<float>(sum / static_cast<double>(rows));
+  }
+}
+
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
@@ -282,7 +295,9 @@ hipError_t launch_plan(const PlanArgs& a, hipStream_t s) {
 hipError_t launch_pool(const PoolArgs& a, int dtype, int head_dim, int64_t grid, hipStream_t s) {
   if (grid <= 0) return hipSuccess;
   const dim3 g(static_cast<unsigned>(grid)), blk(256);
-  if (dtype == FP_DTYPE_BF16) {
+  if (dtype == FP_DTYPE_F32) {
+    hipLaunchKernelGGL(k_pool_f32, g, blk, 0, s, a, head_dim);
+  } else if (dtype == FP_DTYPE_BF16) {
     if (head_dim == 128) hipLaunchKernelGGL((k_pool<BF16, 128>), g, blk, 0, s, a);
     else hipLaunchKernelGGL((k_pool<BF16, 64>), g, blk, 0, s, a);
   } else {

@@ -336,6 +336,116 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
   select_row(pl, ml, n, i, nb, a, list, count, dyn4);
 }
 
+// fp32 inputs: the same row pipeline with fp32 MFMA (v_mfma_f32_32x32x2_f32,
+// full fp32 products; the reference's fp32 path runs tl.dot in TF32). The
+// query block sits in LDS with rows padded by 16 bytes (conflict-free A-operand
+// reads of 32 rows at one column); MFMA k-step s pairs dim s (lanes 0-31)
+// with dim D/2 + s (lanes 32-63), so a lane's key operands are one contiguous
+// half row. Selection is select_row, as for 16-bit inputs.
+template <int D, int BLK>
+__global__ __launch_bounds__(256, 2) void k_search_f32(SearchArgs a) {
+  constexpr int RG = BLK / 32, QS = D + 4, KS = D / 2;
+  extern __shared__ uint4 dyn4[];
+  float* sq = reinterpret_cast<float*>(dyn4);  // BLK rows of QS floats
+  float* pl = sq + BLK * QS;
+  float* ml = pl + a.nb_max;
+  int item, h;
+  map_item(blockIdx.x, a.Hq, item, h);
+  const int64_t nitems = sld(a.tab.seq_tile + a.B);
+  if (item >= nitems) return;
+  const ItemRec rec = sld(a.tab.items + item);
+  const int b = rec.b, i = rec.i, L = rec.L;
+  const int64_t tile_b = rec.tile - i;
+  const int64_t t0 = rec.t0;
+  const int n = i + 1;
+  const int64_t row_tri = static_cast<int64_t>(h) * a.tri_cap + rec.tri;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  const int kvh = h / (a.Hq / a.Hkv);
+  const float c = a.sm_scale_log2;
+  const float* q = reinterpret_cast<const float*>(a.q);
+  const float* mk = reinterpret_cast<const float*>(a.mk) + tile_b * a.Hkv * D + kvh * D;
+
+  // query block -> LDS (rows past the sequence end are zero: they still
+  // count for j < i)
+  for (int cidx = t; cidx < BLK * (D / 4); cidx += 256) {
+    const int r = cidx / (D / 4), x4 = cidx % (D / 4);
+    const int gr = i * BLK + r;
+    float4 val = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (gr < L) val = *reinterpret_cast<const float4*>(q + (t0 + gr) * a.qst + h * a.qhs + 4 * x4);
+    *reinterpret_cast<float4*>(sq + r * QS + 4 * x4) = val;
+  }
+  __syncthreads();
+  const int ntiles = (n + 31) >> 5;
+  for (int tile = w; tile < ntiles; tile += 4) {
+    const int j = 32 * tile + l32;
+    const bool jv = j < n;
+    float kb[KS];
+    const float* kr = mk + static_cast<int64_t>(jv ? j : 0) * a.Hkv * D + half * KS;
+#pragma unroll
+    for (int s4 = 0; s4 < KS / 4; ++s4) {
+      const float4 x = jv ? *reinterpret_cast<const float4*>(kr + 4 * s4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      kb[4 * s4] = x.x; kb[4 * s4 + 1] = x.y; kb[4 * s4 + 2] = x.z; kb[4 * s4 + 3] = x.w;
+    }
+    f32x16 acc[RG];
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg) acc[rg] = f32x16{};
+#pragma unroll
+    for (int s4 = 0; s4 < KS / 4; ++s4)
+#pragma unroll
+      for (int rg = 0; rg < RG; ++rg) {
+        const float4 q4 = *reinterpret_cast<const float4*>(sq + (32 * rg + l32) * QS + half * KS + 4 * s4);
+        acc[rg] = __builtin_amdgcn_mfma_f32_32x32x2f32(q4.x, kb[4 * s4], acc[rg], 0, 0, 0);
+        acc[rg] = __builtin_amdgcn_mfma_f32_32x32x2f32(q4.y, kb[4 * s4 + 1], acc[rg], 0, 0, 0);
+        acc[rg] = __builtin_amdgcn_mfma_f32_32x32x2f32(q4.z, kb[4 * s4 + 2], acc[rg], 0, 0, 0);
+        acc[rg] = __builtin_amdgcn_mfma_f32_32x32x2f32(q4.w, kb[4 * s4 + 3], acc[rg], 0, 0, 0);
+      }
+    // acc[rg][v] = Q[32 rg + 8 (v/4) + 4 half + v%4] . mk[j]; the causal
+    // block rule as in k_search: all rows for j < i, the last row for j == i
+    float mx = -INFINITY, sum = 0.0f;
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc[rg][v]);
+    const bool full = j < i, rowlast = j == i && half == 1;
+    mx = full ? mx : (rowlast ? acc[RG - 1][15] : -INFINITY);
+    const float m = pair32_max(mx) * c;
+#pragma unroll
+    for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sum += __builtin_amdgcn_exp2f(fmaf(acc[rg][v], c, -m));
+    sum = full ? sum : (rowlast ? __builtin_amdgcn_exp2f(fmaf(acc[RG - 1][15], c, -m)) : 0.0f);
+    sum = pair32_sum(sum);
+    if (half == 0 && jv) {
+      pl[j] = sum;
+      ml[j] = m;
+      if (a.dump_p) {
+        a.dump_p[row_tri + j] = sum;
+        a.dump_m[row_tri + j] = m;
+      }
+    }
+  }
+  __syncthreads();
+  int32_t* list = a.idx + row_tri;
+  int32_t* count = a.cnt + static_cast<int64_t>(h) * a.nb_sum_cap + rec.tile;
+  const int nb = static_cast<int>(sld(a.tab.seq_tile + b + 1) - tile_b);
+  select_row(pl, ml, n, i, nb, a, list, count, dyn4);
+}
+
+template <int D, int BLK>
+hipError_t launch_search_f32_t(const SearchArgs& a, int64_t grid, hipStream_t s) {
+  const size_t shm = BLK * (D + 4) * sizeof(float) + 2 * sizeof(float) * static_cast<size_t>(a.nb_max);
+  if (shm > 48 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_search_f32<D, BLK>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(shm));
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((k_search_f32<D, BLK>), dim3(static_cast<unsigned>(grid)), dim3(256), shm, s,
+                     a);
+  return hipGetLastError();
+}
+
 template <typename T, int D, int BLK, bool FROM_SCORES>
 hipError_t launch_search_t(const SearchArgs& a, int64_t grid, hipStream_t s) {
   const size_t shm = search_q_bytes<D, BLK, FROM_SCORES>() +
@@ -364,6 +474,15 @@ hipError_t launch_search_d(const SearchArgs& a, int block, int64_t grid, bool fr
 hipError_t launch_search(const SearchArgs& a, int dtype, int head_dim, int block, int64_t grid,
                          bool from_scores, hipStream_t s) {
   if (grid <= 0) return hipSuccess;
+  if (dtype == FP_DTYPE_F32) {
+    if (from_scores)  // selection only: no input element is read
+      return launch_search_d<BF16, 128>(a, block, grid, true, s);
+    if (head_dim == 128)
+      return block == 128 ? launch_search_f32_t<128, 128>(a, grid, s)
+                          : launch_search_f32_t<128, 64>(a, grid, s);
+    return block == 128 ? launch_search_f32_t<64, 128>(a, grid, s)
+                        : launch_search_f32_t<64, 64>(a, grid, s);
+  }
   if (dtype == FP_DTYPE_BF16)
     return head_dim == 128 ? launch_search_d<BF16, 128>(a, block, grid, from_scores, s)
                            : launch_search_d<BF16, 64>(a, block, grid, from_scores, s);

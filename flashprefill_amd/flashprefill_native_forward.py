@@ -21,8 +21,9 @@ def _readable_in_place(t: torch.Tensor) -> bool:
     """True when (B, S, H, d) packs along tokens with the head dim contiguous
     and 16-byte aligned rows, so the kernels can use it without a copy."""
     S = t.shape[1]
+    vec = 16 // t.element_size()
     return (t.stride(-1) == 1 and t.stride(0) == S * t.stride(1)
-            and t.stride(1) % 8 == 0 and t.stride(2) % 8 == 0 and t.data_ptr() % 16 == 0)
+            and t.stride(1) % vec == 0 and t.stride(2) % vec == 0 and t.data_ptr() % 16 == 0)
 
 
 def _packed_view(t: torch.Tensor) -> torch.Tensor:

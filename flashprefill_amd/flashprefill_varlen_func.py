@@ -16,13 +16,19 @@ import torch
 from .runtime import FlashPrefillCall
 
 
+def _in_place_ok(t: torch.Tensor) -> bool:
+    """Head dim contiguous and 16-byte aligned rows: the kernels read / write
+    ``t`` where it is."""
+    vec = 16 // t.element_size()
+    return (t.stride(-1) == 1 and all(s % vec == 0 for s in t.stride()[:-1])
+            and t.data_ptr() % 16 == 0)
+
+
 def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
-    """Return ``t`` itself when the kernels can read it in place (head dim
-    contiguous, 16-byte aligned rows), else a contiguous copy — the reference
-    forces contiguity for the same purpose (``fla.utils.contiguous``, :580)."""
-    ok = (t.stride(-1) == 1 and all(s % 8 == 0 for s in t.stride()[:-1])
-          and t.data_ptr() % 16 == 0)
-    return t if ok else t.contiguous()
+    """Return ``t`` itself when the kernels can read it in place, else a
+    contiguous copy — the reference forces contiguity for the same purpose
+    (``fla.utils.contiguous``, :580)."""
+    return t if _in_place_ok(t) else t.contiguous()
 
 
 @torch.no_grad()
@@ -43,13 +49,12 @@ def flash_prefill_varlen_func(
     cu_seqlens int32 (B+1,) token offsets; max_seq_len >= every length.
 
     Raises ValueError for malformed arguments and NotImplementedError for
-    arguments the reference accepts but this build does not (fp32 inputs,
-    head_dim other than 64/128, block_size other than 128).
+    arguments the reference accepts but this build does not (head_dim other
+    than 64 / 128, block_size other than 64 / 128).
     """
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     target = o
-    if not (o.stride(-1) == 1 and all(s % 8 == 0 for s in o.stride()[:-1])
-            and o.data_ptr() % 16 == 0):
+    if not _in_place_ok(o):
         # the kernels write a copy of the caller's o; rows of sequences the
         # plan skips (status flags) keep the caller's values after copy-back
         o = torch.empty(o.shape, dtype=o.dtype, device=o.device).copy_(target)

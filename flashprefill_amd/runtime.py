@@ -14,7 +14,8 @@ import torch
 
 from . import _lib
 
-_DTYPES = {torch.bfloat16: _lib.FP_DTYPE_BF16, torch.float16: _lib.FP_DTYPE_F16}
+_DTYPES = {torch.bfloat16: _lib.FP_DTYPE_BF16, torch.float16: _lib.FP_DTYPE_F16,
+           torch.float32: _lib.FP_DTYPE_F32}
 BLOCK = 128
 
 
@@ -58,7 +59,7 @@ def release_workspaces() -> None:
 def _dtype_code(t: torch.Tensor) -> int:
     if t.dtype not in _DTYPES:
         raise NotImplementedError(
-            f"FlashPrefill GPU path supports bfloat16 and float16 inputs, got {t.dtype}")
+            f"FlashPrefill GPU path supports bfloat16, float16 and float32 inputs, got {t.dtype}")
     return _DTYPES[t.dtype]
 
 

@@ -43,11 +43,12 @@ extern "C" {
 
 #define FP_OK 0
 #define FP_E_INVALID_ARG (-1)   /* shapes, strides, alignment or scalars out of range */
-#define FP_E_UNSUPPORTED (-2)   /* valid for the reference but not built here (e.g. fp32) */
+#define FP_E_UNSUPPORTED (-2)   /* valid for the reference but not built here (e.g. block 256) */
 #define FP_E_LAUNCH (-3)        /* a HIP launch or runtime call failed */
 
 #define FP_DTYPE_BF16 0
 #define FP_DTYPE_F16 1
+#define FP_DTYPE_F32 2  /* fp32 kernels (fp32 MFMA); pooled K is fp32 in the workspace */
 
 /* Device-side status flags (`fp_status` word in the workspace, see
  * fp_read_status): set by the kernels when cu_seqlens disagrees with the host
@@ -79,8 +80,8 @@ typedef struct fp_problem {
     int32_t num_q_heads;
     int32_t num_kv_heads;
     int32_t head_dim;      /* 64 or 128 */
-    int32_t dtype;         /* FP_DTYPE_BF16 or FP_DTYPE_F16 */
-    int32_t block_size;    /* 128 */
+    int32_t dtype;         /* FP_DTYPE_BF16, FP_DTYPE_F16 or FP_DTYPE_F32 */
+    int32_t block_size;    /* 64 or 128 */
     /* selection */
     float alpha;
     int32_t attention_sink;
@@ -92,7 +93,7 @@ typedef struct fp_problem {
 
 /* Where each intermediate lives inside the workspace (byte offsets), with the
  * index arithmetic the kernels use:
- *   pooled K   mk[(tile(b) + j) * Hkv * d + kvh * d + x]            (dtype)
+ *   pooled K   mk[(tile(b) + j) * Hkv * d + kvh * d + x]            (input dtype)
  *   counts     cnt[h * nb_sum_cap + tile(b) + i]                    (int32)
  *   lists      idx[h * tri_cap + tri(b) + i*(i+1)/2 + n], n < cnt   (int32, ascending j)
  *   p/m dumps  same triangular index with j in place of n           (fp32)

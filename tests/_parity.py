@@ -16,8 +16,19 @@ OUT_MAX_ABS = 2e-2   # north-star output tolerance (bf16)
 OUT_MEAN_ABS = 2e-3
 
 
+OUT_MAX_ABS_F32 = 1e-4  # fp32 inputs: fp32 MFMA against the oracle's exact-then-rounded dots
+OUT_MEAN_ABS_F32 = 1e-5
+
+
 def ulp_diff_16(a: torch.Tensor, b: torch.Tensor) -> int:
-    """Max distance in units of the last place between two bf16/fp16 tensors."""
+    """Max distance in units of the last place between two bf16 / fp16 (or
+    two fp32) tensors."""
+    if a.dtype == torch.float32:
+        ia = a.contiguous().view(torch.int32).to(torch.int64)
+        ib = b.contiguous().view(torch.int32).to(torch.int64)
+        ia = torch.where(ia < 0, -(2 ** 31) - ia, ia)
+        ib = torch.where(ib < 0, -(2 ** 31) - ib, ib)
+        return int((ia - ib).abs().max().item()) if ia.numel() else 0
     ia = a.contiguous().view(torch.int16).to(torch.int32)
     ib = b.contiguous().view(torch.int16).to(torch.int32)
     # map sign-magnitude to a monotone integer line

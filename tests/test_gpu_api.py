@@ -193,8 +193,11 @@ def test_error_paths():
     T = 256
     q = torch.zeros(T, 4, 128, dtype=torch.float32, device=DEV)
     cu = torch.tensor([0, T], dtype=torch.int32, device=DEV)
-    with pytest.raises(NotImplementedError):
-        flash_prefill_varlen_func(q, q[:, :1], q[:, :1], q.clone(), cu, T, 0.1)
+    with pytest.raises(NotImplementedError):  # float64 is not built
+        flash_prefill_varlen_func(q.double(), q[:, :1].double(), q[:, :1].double(),
+                                  q.double(), cu, T, 0.1)
+    with pytest.raises(ValueError):  # mixed dtypes
+        flash_prefill_varlen_func(q, q[:, :1].to(torch.bfloat16), q[:, :1], q.clone(), cu, T, 0.1)
     qb = q.to(torch.bfloat16)
     with pytest.raises(ValueError):
         flash_prefill_varlen_func(qb, qb[:, :3].contiguous(), qb[:, :3].contiguous(), qb.clone(),
