@@ -184,11 +184,11 @@ __global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
   __shared__ uint4 sk[BLK * CH];
   __shared__ uint4 sv[BLK * CH];
 
-  int item, h;
-  map_item(blockIdx.x, a.Hq, item, h);
   // the item record (one scalar load) carries everything the row needs, so
   // its count and first tile loads follow after one scalar-load latency
   const int64_t nitems = sld(a.tab.seq_tile + a.B);
+  int item, h;
+  map_row(blockIdx.x, a.Hq, a.Hkv, nitems, item, h);
   if (item >= nitems) return;
   const ItemRec rec = sld(a.tab.items + item);
   const int i = rec.i, L = rec.L;

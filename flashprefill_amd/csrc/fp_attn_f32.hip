@@ -37,9 +37,9 @@ __global__ __launch_bounds__(2 * BLK, 1) void k_attn_f32(AttnArgs a) {
   __shared__ float sk[BLK * KSTR];
   __shared__ float sv[BLK * D];
 
-  int item, h;
-  map_item(blockIdx.x, a.Hq, item, h);
   const int64_t nitems = sld(a.tab.seq_tile + a.B);
+  int item, h;
+  map_row(blockIdx.x, a.Hq, a.Hkv, nitems, item, h);
   if (item >= nitems) return;
   const ItemRec rec = sld(a.tab.items + item);
   const int i = rec.i, L = rec.L;

@@ -240,7 +240,7 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   a.Hq = p->num_q_heads;
   a.Hkv = p->num_kv_heads;
   a.sm_scale_log2 = sm_scale_log2(p->head_dim);
-  const int64_t grid = static_cast<int64_t>(p->num_q_heads) * L.nb_sum_cap;
+  const int64_t grid = fp::attn_grid(p->num_q_heads, p->num_kv_heads, L.nb_sum_cap);
   const hipError_t e =
       p->dtype == FP_DTYPE_F32
           ? fp::launch_attn_f32(a, p->head_dim, p->block_size, grid, s)

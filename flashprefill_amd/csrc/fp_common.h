@@ -125,6 +125,38 @@ __device__ __forceinline__ int find_seq(const int64_t* seq_tile, int B, int64_t 
   return lo;
 }
 
+// Attention rows. Per-row cost depends on the row's selection, whose density
+// differs between heads, so a fixed head -> XCD assignment leaves some XCDs
+// with more work than others (10 % at 128K in config 3). When the number of
+// KV heads divides 8, the XCDs are split into Hkv sets of R = 8 / Hkv; a set
+// serves one GQA group at a time (its G query heads share K / V, which its L2
+// holds) and its XCDs take consecutive q-blocks in turn; every `per` q-block
+// rounds the sets move on to the next group, so that over the sequence each
+// set serves every group 4 times and the XCDs end with equal shares. Rows are
+// still walked heaviest first within each XCD. attn_grid() is the matching
+// grid size (workgroups past the last row return at once).
+__device__ __forceinline__ void map_row(int w, int num_q_heads, int num_kv_heads, int64_t nitems,
+                                        int& item, int& head) {
+  if ((8 % num_kv_heads) == 0) {
+    const int x = w & 7, s = w >> 3;
+    const int R = 8 / num_kv_heads, G = num_q_heads / num_kv_heads;
+    const int p = s / G, r = s % G;
+    const int per = max(4, static_cast<int>(nitems / R / (4 * num_kv_heads)));
+    item = R * p + x % R;
+    head = ((x / R + p / per) % num_kv_heads) * G + r;
+  } else {
+    map_item(w, num_q_heads, item, head);
+  }
+}
+
+inline int64_t attn_grid(int num_q_heads, int num_kv_heads, int64_t nitems_cap) {
+  if ((8 % num_kv_heads) == 0) {
+    const int64_t R = 8 / num_kv_heads;
+    return 8 * static_cast<int64_t>(num_q_heads / num_kv_heads) * ((nitems_cap + R - 1) / R);
+  }
+  return static_cast<int64_t>(num_q_heads) * nitems_cap;
+}
+
 // One work item as the plan kernel records it (32 bytes, read with one scalar
 // load by the persistent attention kernel).
 struct ItemRec {
