@@ -25,7 +25,7 @@ FP_DTYPE_F16 = 1
 FP_DTYPE_F32 = 2
 FP_STATUS_SEQ_TOO_LONG = 1
 FP_STATUS_BAD_CU_SEQLENS = 2
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 EXPORTS = (
     "fp_workspace_layout", "fp_workspace_bytes", "fp_flashprefill", "fp_plan", "fp_pool_k",
@@ -63,7 +63,8 @@ class FpWsLayout(ctypes.Structure):
         ("seq_start_off", ctypes.c_size_t), ("seq_len_off", ctypes.c_size_t),
         ("items_off", ctypes.c_size_t),
         ("mk_off", ctypes.c_size_t),
-        ("cnt_off", ctypes.c_size_t), ("idx_off", ctypes.c_size_t),
+        ("cnt_off", ctypes.c_size_t), ("rowrec_off", ctypes.c_size_t),
+        ("idx_off", ctypes.c_size_t),
         ("nb_sum_cap", ctypes.c_int64), ("tri_cap", ctypes.c_int64),
         ("nb_max", ctypes.c_int32),
     ]

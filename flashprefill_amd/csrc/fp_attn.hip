@@ -184,19 +184,26 @@ __global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
   __shared__ uint4 sk[BLK * CH];
   __shared__ uint4 sv[BLK * CH];
 
-  // the item record (one scalar load) carries everything the row needs, so
-  // its count and first tile loads follow after one scalar-load latency
-  const int64_t nitems = sld(a.tab.seq_tile + a.B);
+  // the item record, the row record written by the selection stage (count,
+  // first two list entries, diagonal kept) and the item count are three
+  // independent scalar loads, so the row's first tile loads follow after one
+  // scalar-load latency
   int item, h;
-  map_row(blockIdx.x, a.Hq, a.Hkv, nitems, item, h);
+  map_row(blockIdx.x, a.Hq, a.Hkv, a.nb_sum_cap, item, h);
+  const int64_t nitems = sld(a.tab.seq_tile + a.B);
+  // map_row can return items up to 8 / Hkv - 1 past the table's capacity;
+  // those (and any item >= nitems) return below, so the loads are clamped
+  const int64_t it = min(static_cast<int64_t>(item), a.nb_sum_cap - 1);
+  const ItemRec rec = sld(a.tab.items + it);
+  const int4 rrec = sld(reinterpret_cast<const int4*>(a.rowrec) +
+                        static_cast<int64_t>(h) * a.nb_sum_cap + it);
   if (item >= nitems) return;
-  const ItemRec rec = sld(a.tab.items + item);
   const int i = rec.i, L = rec.L;
   const int64_t t0 = rec.t0;
   const int64_t row_tri = static_cast<int64_t>(h) * a.tri_cap + rec.tri;
-  // counts and lists come from the search stage; clamp them to the row's
+  // counts and entries come from the search stage; clamp them to the row's
   // capacity so a stale workspace can never index outside the sequence
-  const int ncnt = min(max(sld(a.cnt + static_cast<int64_t>(h) * a.nb_sum_cap + rec.tile), 0), i + 1);
+  const int ncnt = min(max(rrec.x, 0), i + 1);
   const int32_t* list = a.idx + row_tri;
   const int kvh = h / (a.Hq / a.Hkv);
 
@@ -211,12 +218,11 @@ __global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
   const uint16_t* kbase = a.k + t0 * a.kst + static_cast<int64_t>(kvh) * a.khs;
   const uint16_t* vbase = a.v + t0 * a.vst + static_cast<int64_t>(kvh) * a.vhs;
 
-  auto list_at = [&](int n) { return min(max(sld(list + n), 0), i); };
   TileLanes<D, BLK, NW> tk, tv;
   tk.init(a.kst, w, lane);
   tv.init(a.vst, w, lane);
   if (ncnt > 0) {
-    const int j0 = list_at(0);
+    const int j0 = min(max(rrec.y, 0), i);
     issue_tile<D, BLK, NW>(sk, kbase, a.kst, tk, j0, L, w, lane);
     issue_tile<D, BLK, NW>(sv, vbase, a.vst, tv, j0, L, w, lane);
   }
@@ -248,11 +254,11 @@ __global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
 
   const uint16_t* sv16 = reinterpret_cast<const uint16_t*>(sv);
   // the diagonal block, when selected, is the last entry of the ascending list
-  const bool has_diag = ncnt > 0 && list_at(ncnt - 1) == i;
+  const bool has_diag = ncnt > 0 && rrec.w != 0;
   const int nplain = ncnt - (has_diag ? 1 : 0);
   // block n refills the buffers with entry n + 1 and prefetches entry n + 2
   // (entry ncnt - 1 past the end of the list; not used then)
-  int jraw = ncnt > 1 ? sld(list + 1) : 0;
+  int jraw = ncnt > 1 ? rrec.z : 0;
   for (int n = 0; n < nplain; ++n) {
     const int jn = n + 1 < ncnt ? min(max(jraw, 0), i) : -1;
     attn_block<T, D, BLK, false>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv, jn,

@@ -39,7 +39,7 @@ __global__ __launch_bounds__(2 * BLK, 1) void k_attn_f32(AttnArgs a) {
 
   const int64_t nitems = sld(a.tab.seq_tile + a.B);
   int item, h;
-  map_row(blockIdx.x, a.Hq, a.Hkv, nitems, item, h);
+  map_row(blockIdx.x, a.Hq, a.Hkv, a.nb_sum_cap, item, h);
   if (item >= nitems) return;
   const ItemRec rec = sld(a.tab.items + item);
   const int i = rec.i, L = rec.L;

@@ -112,6 +112,7 @@ int layout(const fp_problem* p, fp_ws_layout* L) {
   L->items_off = off;      off = align_up(off + sizeof(fp::ItemRec) * cap);
   L->mk_off = off;         off = align_up(off + eb * cap * Hkv * d);
   L->cnt_off = off;        off = align_up(off + 4 * Hq * cap);
+  L->rowrec_off = off;     off = align_up(off + 16 * Hq * cap);
   L->idx_off = off;        off = align_up(off + 4 * Hq * tri);
   L->total_bytes = off;
   return FP_OK;
@@ -185,6 +186,7 @@ fp::SearchArgs search_args(const fp_problem* p, const fp_ws_layout& L, void* ws)
   a.mk = reinterpret_cast<const uint16_t*>(base + L.mk_off);
   a.idx = reinterpret_cast<int32_t*>(base + L.idx_off);
   a.cnt = reinterpret_cast<int32_t*>(base + L.cnt_off);
+  a.rowrec = reinterpret_cast<int32_t*>(base + L.rowrec_off);
   a.tri_cap = L.tri_cap;
   a.nb_sum_cap = L.nb_sum_cap;
   a.B = p->batch;
@@ -234,6 +236,7 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   a.ohs = p->o_stride_head;
   a.idx = reinterpret_cast<const int32_t*>(base + L.idx_off);
   a.cnt = reinterpret_cast<const int32_t*>(base + L.cnt_off);
+  a.rowrec = reinterpret_cast<const int32_t*>(base + L.rowrec_off);
   a.tri_cap = L.tri_cap;
   a.nb_sum_cap = L.nb_sum_cap;
   a.B = p->batch;
@@ -287,7 +290,7 @@ int scratch_on_current_device(void** out) {
 
 extern "C" {
 
-int fp_abi_version(void) { return 3; }
+int fp_abi_version(void) { return 4; }
 
 const char* fp_last_error(void) { return g_last_error.c_str(); }
 

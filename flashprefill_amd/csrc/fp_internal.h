@@ -36,6 +36,7 @@ struct SearchArgs {
   const uint16_t* mk;
   int32_t* idx;
   int32_t* cnt;
+  int32_t* rowrec;    // per (head, item): {count, first entry, second entry, diagonal kept}
   int64_t tri_cap;
   int64_t nb_sum_cap;
   const float* in_p;  // select-only mode: caller's block scores
@@ -57,6 +58,7 @@ struct AttnArgs {
   int64_t qst, qhs, kst, khs, vst, vhs, ost, ohs;
   const int32_t* idx;
   const int32_t* cnt;
+  const int32_t* rowrec;  // per (head, item): {count, first entry, second entry, diagonal kept}
   int64_t tri_cap;
   int64_t nb_sum_cap;
   int32_t B, Hq, Hkv;

@@ -39,7 +39,7 @@ __device__ __forceinline__ uint32_t sort_key(float f) {
 }
 
 // LDS scratch of select_row: block-reduction slots and the radix histogram
-constexpr int kSelectScratch = 64 + 32 + 256 * 4;
+constexpr int kSelectScratch = 104 + 256 * 4;
 
 // The min_budget largest scores of a row, ranked by (score desc, j asc) as
 // the oracle ranks them (native path, ops/flashprefill_native_forward.py:
@@ -105,14 +105,16 @@ __device__ uint32_t budget_threshold(const float* pl, int n, int kk, uint32_t* h
 // max. The compaction loops use alternating count slots, one barrier per
 // 256 entries.
 __device__ void select_row(float* pl, float* ml, int n, int i, int nb, const SearchArgs& a,
-                           int32_t* list, int32_t* count, void* scratch) {
+                           int32_t* list, int32_t* count, int32_t* row_rec, void* scratch) {
 #pragma clang fp contract(off)
   float* redf = static_cast<float*>(scratch);
   double* redd = reinterpret_cast<double*>(static_cast<char*>(scratch) + 16);
   int* wtot = reinterpret_cast<int*>(static_cast<char*>(scratch) + 48);  // [2][4]
   int* pick = reinterpret_cast<int*>(static_cast<char*>(scratch) + 80);
-  uint32_t* hist = reinterpret_cast<uint32_t*>(static_cast<char*>(scratch) + 96);
+  int* head3 = reinterpret_cast<int*>(static_cast<char*>(scratch) + 88);  // row record: j0, j1, diag
+  uint32_t* hist = reinterpret_cast<uint32_t*>(static_cast<char*>(scratch) + 104);
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  if (t < 3) head3[t] = 0;
 
   float lm = -INFINITY;
   for (int j = t; j < n; j += 256) lm = fmaxf(lm, ml[j]);
@@ -178,10 +180,21 @@ __device__ void select_row(float* pl, float* ml, int n, int i, int nb, const Sea
     __syncthreads();
     int off = running;
     for (int k = 0; k < w; ++k) off += wtot[c2 + k];
-    if (keep) list[off + lanes_below(bal)] = j;
+    if (keep) {
+      const int pos = off + lanes_below(bal);
+      list[pos] = j;
+      if (pos < 2) head3[pos] = j;
+    }
+    if (j == i) head3[2] = keep ? 1 : 0;
     running += wtot[c2] + wtot[c2 + 1] + wtot[c2 + 2] + wtot[c2 + 3];
   }
-  if (t == 0) *count = running;
+  __syncthreads();  // head3 complete
+  if (t == 0) {
+    *count = running;
+    // the attention kernel's row record: one 16-byte load gives the count,
+    // the first two entries and whether the diagonal block is kept
+    *reinterpret_cast<int4*>(row_rec) = make_int4(running, head3[0], head3[1], head3[2]);
+  }
 }
 
 // LDS chunk swizzle of a 128 x D bf16 tile (16-byte chunks; conflict-free
@@ -332,8 +345,9 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
   __syncthreads();
   int32_t* list = a.idx + row_tri;
   int32_t* count = a.cnt + static_cast<int64_t>(h) * a.nb_sum_cap + rec.tile;
+  int32_t* row_rec = a.rowrec + 4 * (static_cast<int64_t>(h) * a.nb_sum_cap + item);
   const int nb = static_cast<int>(sld(a.tab.seq_tile + b + 1) - tile_b);
-  select_row(pl, ml, n, i, nb, a, list, count, dyn4);
+  select_row(pl, ml, n, i, nb, a, list, count, row_rec, dyn4);
 }
 
 // fp32 inputs: the same row pipeline with fp32 MFMA (v_mfma_f32_32x32x2_f32,
@@ -428,8 +442,9 @@ __global__ __launch_bounds__(256, 2) void k_search_f32(SearchArgs a) {
   __syncthreads();
   int32_t* list = a.idx + row_tri;
   int32_t* count = a.cnt + static_cast<int64_t>(h) * a.nb_sum_cap + rec.tile;
+  int32_t* row_rec = a.rowrec + 4 * (static_cast<int64_t>(h) * a.nb_sum_cap + item);
   const int nb = static_cast<int>(sld(a.tab.seq_tile + b + 1) - tile_b);
-  select_row(pl, ml, n, i, nb, a, list, count, dyn4);
+  select_row(pl, ml, n, i, nb, a, list, count, row_rec, dyn4);
 }
 
 template <int D, int BLK>

@@ -112,6 +112,8 @@ typedef struct fp_ws_layout {
                             int64 seq_start, seq_tri[b] + i (i + 1) / 2 */
     size_t mk_off;
     size_t cnt_off;
+    size_t rowrec_off;   /* int32[Hq * nb_sum_cap][4] by (head, item): count, first and
+                            second list entry, diagonal block kept */
     size_t idx_off;
     int64_t nb_sum_cap;  /* >= sum_b NB_b */
     int64_t tri_cap;     /* >= sum_b NB_b (NB_b + 1) / 2 */

@@ -63,7 +63,7 @@ def test_layout_bounds():
     cap = L.nb_sum_cap
     assert L.tri_cap == (cap // 32) * 32 * 33 // 2 + (cap % 32) * (cap % 32 + 1) // 2
     offs = [L.status_off, L.seq_tile_off, L.seq_tri_off, L.seq_start_off, L.seq_len_off,
-            L.items_off, L.mk_off, L.cnt_off, L.idx_off]
+            L.items_off, L.mk_off, L.cnt_off, L.rowrec_off, L.idx_off]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
     assert L.total_bytes >= L.idx_off + 4 * 8 * L.tri_cap
     assert _lib.load().fp_workspace_bytes(ctypes.byref(_problem())) == L.total_bytes
