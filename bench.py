@@ -59,6 +59,12 @@ def parse():
                          "sampling socket power with amd-smi; print time, power and energy "
                          "per launch")
     ap.add_argument("--power-seconds", type=float, default=4.0)
+    ap.add_argument("--attn-sweep", action="store_true",
+                    help="attention stage alone at 128K over selection settings: a window sweep "
+                         "(alpha 1, last-n 0; linear fit of time against blocks per row gives "
+                         "the per-block and per-row cost), the bench setting, a near-dense "
+                         "alpha and every block (alpha 0); one JSON line per setting, for "
+                         "clock counters under rocprofv3")
     return ap.parse_args()
 
 
@@ -261,6 +267,45 @@ def power_run(args):
                       "launches": n, "ms_per_launch": round(ms, 4), "power_samples": len(watts),
                       "socket_power_W_median": w,
                       "energy_J_per_launch": round(w * ms / 1e3, 3) if w else None}), flush=True)
+
+
+def attn_sweep(args):
+    """Attention stage at --seq-len over several selections (see --attn-sweep)."""
+    import statistics
+    import torch
+    from flashprefill_amd import synth
+    from flashprefill_amd.runtime import FlashPrefillCall
+    dev = torch.device("cuda:0")
+    S = args.seq_len
+    spec = synth.llama_spec(S, seed=args.seed)
+    q, k, v, cu = synth.make_inputs(spec, device=dev)
+    o = torch.empty_like(q)
+    rows = spec.num_q_heads * ((S + 127) // 128)
+    fit = []
+    cases = [dict(alpha=1.0, window_size=w, last_n_block=0) for w in (1, 2, 4, 8, 16, 32, 64)]
+    cases += [dict(alpha=args.alpha, window_size=4, last_n_block=2),
+              dict(alpha=0.01, window_size=4, last_n_block=2),
+              dict(alpha=0.0, window_size=4, last_n_block=2)]
+    for cs in cases:
+        call = FlashPrefillCall(q, k, v, o, cu, S, **cs)
+        call.plan(); call.pool(); call.search(); call.attn()
+        n = int(call.counts()[:, :rows // spec.num_q_heads].sum().item())
+        ms = median([timed(call.attn, 3 if cs["alpha"] else 1) for _ in range(3)])
+        rec = dict(cs, blocks=n, blocks_per_row=round(n / rows, 3), ms_attn=round(ms, 4),
+                   executed_tflops=round(4 * 128 * 128 * spec.head_dim * n / ms / 1e9, 1))
+        print(json.dumps(rec), flush=True)
+        if cs["alpha"] == 1.0:
+            fit.append((n / rows, ms))
+    xs, ys = [x for x, _ in fit], [y for _, y in fit]
+    mx, my = statistics.mean(xs), statistics.mean(ys)
+    slope = sum((x - mx) * (y - my) for x, y in zip(xs, ys)) / sum((x - mx) ** 2 for x in xs)
+    # one row per (head, q-block); time per row and per block in slot units:
+    # rows * cost / (2 workgroups per CU x CUs)
+    slots = 2 * torch.cuda.get_device_properties(dev).multi_processor_count
+    print(json.dumps({"window_sweep_fit": {
+        "us_per_block_per_slot": round(slope * 1e3 * slots / rows, 3),
+        "us_per_row_per_slot": round((my - slope * mx) * 1e3 * slots / rows, 3),
+        "slots": slots}}), flush=True)
 
 
 def dense_causal_flops(S, Hq, d):
@@ -603,6 +648,9 @@ def main():
         return
     if args.power:
         power_run(args)
+        return
+    if args.attn_sweep:
+        attn_sweep(args)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (one MI355X per box); "
