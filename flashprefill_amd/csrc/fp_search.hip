@@ -5,11 +5,12 @@
 //  1. score (ops/flashprefill_native_forward.py:87-188,
 //     ops/flashprefill_varlen_func.py:106-217): the 128 full-resolution query
 //     rows of block i against every pooled key j <= i on bf16/fp16 MFMA
-//     (v_mfma_f32_32x32x16), S = Q . mk^T. Each wave keeps the whole 128 x d Q
-//     block in registers as A operands and walks its own 32-column tiles of
-//     pooled keys, so the per-column reductions over the 128 rows
+//     (v_mfma_f32_32x32x16), S = Q . mk^T. The query block is staged once in
+//     LDS (direct-to-LDS loads, chunk-swizzled) and every wave reads it as
+//     MFMA A operands while it walks its own 32-column tiles of pooled keys
+//     (B operands from L2), so the per-column reductions over the block's rows
 //     (m_ij = max_r s_r, p_ij = sum_r exp2(s_r - m_ij)) are in-register plus
-//     one cross-half exchange; nothing is shared between waves. The causal
+//     one cross-half exchange; no partial result is shared between waves. The causal
 //     block rule keeps all rows for j < i and only row 127 for j == i (:157).
 //     (p, m) of the row stay in LDS (optionally dumped to global for parity
 //     tests).
