@@ -25,14 +25,14 @@ FP_DTYPE_F16 = 1
 FP_DTYPE_F32 = 2
 FP_STATUS_SEQ_TOO_LONG = 1
 FP_STATUS_BAD_CU_SEQLENS = 2
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 EXPORTS = (
     "fp_workspace_layout", "fp_workspace_bytes", "fp_flashprefill", "fp_plan", "fp_pool_k",
     "fp_search", "fp_select", "fp_sparse_attn_fwd", "fp_read_status", "fp_last_error",
     "fp_abi_version", "fp_flashprefill_noalloc", "fp_kv_cache_write",
 )
-NOALLOC_SCRATCH_BYTES = 80 * 1024 * 1024
+NOALLOC_SCRATCH_BYTES = 96 * 1024 * 1024
 
 
 class FpProblem(ctypes.Structure):
@@ -64,9 +64,11 @@ class FpWsLayout(ctypes.Structure):
         ("items_off", ctypes.c_size_t),
         ("mk_off", ctypes.c_size_t),
         ("cnt_off", ctypes.c_size_t), ("rowrec_off", ctypes.c_size_t),
-        ("idx_off", ctypes.c_size_t),
+        ("idx_off", ctypes.c_size_t), ("units_off", ctypes.c_size_t),
+        ("part_off", ctypes.c_size_t),
         ("nb_sum_cap", ctypes.c_int64), ("tri_cap", ctypes.c_int64),
-        ("nb_max", ctypes.c_int32),
+        ("unit_cap", ctypes.c_int64),
+        ("nb_max", ctypes.c_int32), ("split_blocks", ctypes.c_int32),
     ]
 
 

@@ -184,27 +184,59 @@ __global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
   __shared__ uint4 sk[BLK * CH];
   __shared__ uint4 sv[BLK * CH];
 
-  // the item record, the row record written by the selection stage (count,
-  // first two list entries, diagonal kept) and the item count are three
-  // independent scalar loads, so the row's first tile loads follow after one
-  // scalar-load latency
-  int item, h;
-  map_row(blockIdx.x, a.Hq, a.Hkv, a.nb_sum_cap, item, h);
-  const int64_t nitems = sld(a.tab.seq_tile + a.B);
-  // map_row can return items up to 8 / Hkv - 1 past the table's capacity;
-  // those (and any item >= nitems) return below, so the loads are clamped
-  const int64_t it = min(static_cast<int64_t>(item), a.nb_sum_cap - 1);
-  const ItemRec rec = sld(a.tab.items + it);
-  const int4 rrec = sld(reinterpret_cast<const int4*>(a.rowrec) +
-                        static_cast<int64_t>(h) * a.nb_sum_cap + it);
-  if (item >= nitems) return;
+  // Work item: the first unit_slots workgroups take the chunks of the split
+  // rows (a slice of a dense row's list, fp32 partials out), the others one
+  // (head, sequence, q-block) row each through map_row. For a row, the item
+  // record, the row record written by the selection stage (count, first two
+  // list entries, diagonal kept) and the item count are three independent
+  // scalar loads, so the row's first tile loads follow after one scalar-load
+  // latency.
+  ItemRec rec;
+  int h, ncnt, j0, jraw, unit = -1;
+  bool has_diag;
+  int64_t first = 0;  // list offset of the chunk
+  if (static_cast<int64_t>(blockIdx.x) < a.unit_slots) {
+    int u;
+    map_item(blockIdx.x, a.Hq, u, h);
+    const int nunits = sld(a.units);
+    if (u >= nunits) return;
+    const UnitRec ur =
+        sld(reinterpret_cast<const UnitRec*>(reinterpret_cast<const char*>(a.units) + 64) + u);
+    rec = ur.r;
+    // a split row selects every causal block, so its list is 0 .. i and the
+    // chunk's entries are first .. first + ncnt - 1; the diagonal block is the
+    // last chunk's last entry
+    first = static_cast<int64_t>(ur.c) * a.split_blocks;
+    ncnt = max(min(a.split_blocks, rec.i + 1 - static_cast<int>(first)), 0);
+    j0 = static_cast<int>(first);
+    jraw = j0 + 1;
+    has_diag = ncnt > 0 && ur.c == ur.nc - 1;
+    unit = u;
+  } else {
+    int item;
+    map_row(static_cast<int>(blockIdx.x - a.unit_slots), a.Hq, a.Hkv, a.nb_sum_cap, item, h);
+    const int64_t nitems = sld(a.tab.seq_tile + a.B);
+    // map_row can return items up to 8 / Hkv - 1 past the table's capacity;
+    // those (and any item >= nitems) return below, so the loads are clamped
+    const int64_t it = min(static_cast<int64_t>(item), a.nb_sum_cap - 1);
+    rec = sld(a.tab.items + it);
+    const int4 rrec = sld(reinterpret_cast<const int4*>(a.rowrec) +
+                          static_cast<int64_t>(h) * a.nb_sum_cap + it);
+    if (item >= nitems) return;
+    // the chunks of a split row produce its output
+    if (row_is_split(rec.i, (rec.L + BLK - 1) / BLK, a.last_n, a.split_blocks)) return;
+    // counts and entries come from the search stage; clamp them to the row's
+    // capacity so a stale workspace can never index outside the sequence
+    ncnt = min(max(rrec.x, 0), rec.i + 1);
+    j0 = rrec.y;
+    jraw = ncnt > 1 ? rrec.z : 0;
+    // the diagonal block, when selected, is the last entry of the ascending list
+    has_diag = ncnt > 0 && rrec.w != 0;
+  }
   const int i = rec.i, L = rec.L;
   const int64_t t0 = rec.t0;
   const int64_t row_tri = static_cast<int64_t>(h) * a.tri_cap + rec.tri;
-  // counts and entries come from the search stage; clamp them to the row's
-  // capacity so a stale workspace can never index outside the sequence
-  const int ncnt = min(max(rrec.x, 0), i + 1);
-  const int32_t* list = a.idx + row_tri;
+  const int32_t* list = a.idx + row_tri + first;
   const int kvh = h / (a.Hq / a.Hkv);
 
   const int t = threadIdx.x, lane = t & 63;
@@ -222,9 +254,9 @@ __global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
   tk.init(a.kst, w, lane);
   tv.init(a.vst, w, lane);
   if (ncnt > 0) {
-    const int j0 = min(max(rrec.y, 0), i);
-    issue_tile<D, BLK, NW>(sk, kbase, a.kst, tk, j0, L, w, lane);
-    issue_tile<D, BLK, NW>(sv, vbase, a.vst, tv, j0, L, w, lane);
+    const int jc = min(max(j0, 0), i);
+    issue_tile<D, BLK, NW>(sk, kbase, a.kst, tk, jc, L, w, lane);
+    issue_tile<D, BLK, NW>(sv, vbase, a.vst, tv, jc, L, w, lane);
   }
   // Q^T as MFMA B operand (lane: query l32, dims 16 s + 8 half .. +7), loaded
   // after the first block's tile loads and waited for here, so one memory
@@ -253,12 +285,9 @@ __global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
   st.l_part = half == 0 ? 1.0f : 0.0f;  // the two halves' partial sums add up to l
 
   const uint16_t* sv16 = reinterpret_cast<const uint16_t*>(sv);
-  // the diagonal block, when selected, is the last entry of the ascending list
-  const bool has_diag = ncnt > 0 && rrec.w != 0;
   const int nplain = ncnt - (has_diag ? 1 : 0);
   // block n refills the buffers with entry n + 1 and prefetches entry n + 2
   // (entry ncnt - 1 past the end of the list; not used then)
-  int jraw = ncnt > 1 ? rrec.z : 0;
   for (int n = 0; n < nplain; ++n) {
     const int jn = n + 1 < ncnt ? min(max(jraw, 0), i) : -1;
     attn_block<T, D, BLK, false>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv, jn,
@@ -271,6 +300,24 @@ __global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
   }
 
   const float l = pair32_sum(st.l_part);
+  if (unit >= 0) {
+    // chunk of a split row: unnormalised O^T, the running max and l, for k_merge
+    float* pp = a.part + (static_cast<int64_t>(h) * a.unit_cap + unit) *
+                             static_cast<int64_t>(BLK * D + 2 * BLK);
+    float* orow = pp + static_cast<int64_t>(qrow) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4)
+        *reinterpret_cast<float4*>(orow + 32 * dt + 8 * g4 + 4 * half) =
+            make_float4(st.o[dt][4 * g4], st.o[dt][4 * g4 + 1], st.o[dt][4 * g4 + 2],
+                        st.o[dt][4 * g4 + 3]);
+    if (half == 0) {
+      pp[BLK * D + qrow] = st.m_run;
+      pp[BLK * D + BLK + qrow] = l;
+    }
+    return;
+  }
   const float rcp = 1.0f / l;
   if (qvalid) {
     uint16_t* op = a.o + (t0 + qg) * a.ost + static_cast<int64_t>(h) * a.ohs;
@@ -287,12 +334,101 @@ __global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
   }
 }
 
+// Output rows of the split rows. Workgroup (slot, s) of the grid
+// (unit_slots x BLK / 32) takes query rows 32 s .. 32 s + 31 of the unit that
+// k_attn's chunk slot `slot` ran; only a row's first chunk's slots work. Eight
+// threads per query row, D / 8 dims each: every load of a thread (the chunks'
+// m and l, then its slice of each chunk's O) is issued before any is used, so
+// the merge costs about one memory latency. Flash-decoding merge:
+// m = max_c m_c, w_c = exp2(m_c - m), O = sum_c w_c acc_c / sum_c w_c l_c.
+template <typename T, int D, int BLK>
+__global__ __launch_bounds__(256) void k_merge(AttnArgs a) {
+  constexpr int XT = D / 8;        // dims per thread
+  constexpr int MAXC = 4;          // chunks per split row (host policy)
+  const int slot = static_cast<int>(blockIdx.x / (BLK / 32));
+  const int s = static_cast<int>(blockIdx.x % (BLK / 32));
+  int u, h;
+  map_item(slot, a.Hq, u, h);
+  const int nunits = sld(a.units);
+  if (u >= nunits) return;
+  const UnitRec ur =
+      sld(reinterpret_cast<const UnitRec*>(reinterpret_cast<const char*>(a.units) + 64) + u);
+  if (ur.c != 0) return;
+  const int nc = min(min(ur.nc, nunits - u), MAXC);
+  const int r = 32 * s + static_cast<int>(threadIdx.x >> 3);
+  const int x0 = XT * static_cast<int>(threadIdx.x & 7);
+  const int qg = ur.r.i * BLK + r;
+  if (qg >= ur.r.L) return;
+  const int64_t S = BLK * D + 2 * BLK;  // floats per partial
+  const float* p0 = a.part + (static_cast<int64_t>(h) * a.unit_cap + u) * S;
+  float mc[MAXC], lc[MAXC];
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    mc[c] = c < nc ? p0[c * S + BLK * D + r] : -INFINITY;
+    lc[c] = c < nc ? p0[c * S + BLK * D + BLK + r] : 0.0f;
+  }
+  float4 oc[MAXC][XT / 4];
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c)
+#pragma unroll
+    for (int q = 0; q < XT / 4; ++q)
+      oc[c][q] = c < nc ? *reinterpret_cast<const float4*>(p0 + c * S + static_cast<int64_t>(r) * D +
+                                                          x0 + 4 * q)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+  float m = mc[0];
+#pragma unroll
+  for (int c = 1; c < MAXC; ++c) m = fmaxf(m, mc[c]);
+  float wc[MAXC], lsum = 0.0f;
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    wc[c] = c < nc ? __builtin_amdgcn_exp2f(mc[c] - m) : 0.0f;
+    lsum += wc[c] * lc[c];
+  }
+  const float rcp = 1.0f / lsum;
+  uint16_t* op = a.o + (ur.r.t0 + qg) * a.ost + static_cast<int64_t>(h) * a.ohs + x0;
+#pragma unroll
+  for (int q = 0; q < XT / 4; ++q) {
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      acc.x += wc[c] * oc[c][q].x;
+      acc.y += wc[c] * oc[c][q].y;
+      acc.z += wc[c] * oc[c][q].z;
+      acc.w += wc[c] * oc[c][q].w;
+    }
+    uint2 pk;
+    pk.x = pack2<T>(acc.x * rcp, acc.y * rcp);
+    pk.y = pack2<T>(acc.z * rcp, acc.w * rcp);
+    *reinterpret_cast<uint2*>(op + 4 * q) = pk;
+  }
+}
+
 template <typename T, int D>
 hipError_t launch_attn_t(const AttnArgs& a, int block, int64_t grid, hipStream_t s) {
   const dim3 g(static_cast<unsigned>(grid));
   if (block == 128) hipLaunchKernelGGL((k_attn<T, D, 128>), g, dim3(256), 0, s, a);
   else hipLaunchKernelGGL((k_attn<T, D, 64>), g, dim3(128), 0, s, a);
   return hipGetLastError();
+}
+
+template <typename T, int D>
+hipError_t launch_merge_t(const AttnArgs& a, int block, hipStream_t s) {
+  if (block == 128)
+    hipLaunchKernelGGL((k_merge<T, D, 128>), dim3(static_cast<unsigned>(a.unit_slots * 4)),
+                       dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((k_merge<T, D, 64>), dim3(static_cast<unsigned>(a.unit_slots * 2)),
+                       dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_merge(const AttnArgs& a, int dtype, int head_dim, int block, hipStream_t s) {
+  if (a.unit_slots <= 0 || dtype == FP_DTYPE_F32) return hipSuccess;
+  if (dtype == FP_DTYPE_BF16)
+    return head_dim == 128 ? launch_merge_t<BF16, 128>(a, block, s)
+                           : launch_merge_t<BF16, 64>(a, block, s);
+  return head_dim == 128 ? launch_merge_t<F16, 128>(a, block, s)
+                         : launch_merge_t<F16, 64>(a, block, s);
 }
 
 hipError_t launch_attn(const AttnArgs& a, int dtype, int head_dim, int block, int64_t grid,

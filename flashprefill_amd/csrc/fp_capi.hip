@@ -11,6 +11,8 @@
 #include <mutex>
 #include <string>
 
+#include <algorithm>
+
 #include "fp_internal.h"
 
 namespace {
@@ -114,6 +116,27 @@ int layout(const fp_problem* p, fp_ws_layout* L) {
   L->cnt_off = off;        off = align_up(off + 4 * Hq * cap);
   L->rowrec_off = off;     off = align_up(off + 16 * Hq * cap);
   L->idx_off = off;        off = align_up(off + 4 * Hq * tri);
+  // Split rows (16-bit inputs, fp::UnitRec): a last_n row selects every causal
+  // block, so with one workgroup per row it outlasts the rest of the attention
+  // at short and mid lengths. Rows of more than C = max(8, ceil(NB / 4))
+  // blocks run as up to 4 chunks of C blocks; at most min(B, cap / (C + 1))
+  // sequences have more than C blocks. Batches of many long sequences balance
+  // without it (and would need large partial buffers), so it is off there.
+  int64_t split = 0, units = 0;
+  if (p->dtype != FP_DTYPE_F32 && p->last_n_block > 0) {
+    split = std::max<int64_t>(8, (nb_max + 3) / 4);
+    if (nb_max > split) {
+      const int64_t seqs = std::min<int64_t>(B, cap / (split + 1));
+      const int64_t rows = seqs * std::min<int64_t>(p->last_n_block, nb_max);
+      units = rows * ((nb_max + split - 1) / split);
+      if (units * Hq > 65536) units = 0;
+    }
+    if (units == 0) split = 0;
+  }
+  L->split_blocks = static_cast<int32_t>(split);
+  L->unit_cap = units;
+  L->units_off = off;      off = align_up(off + 64 + sizeof(fp::UnitRec) * units);
+  L->part_off = off;       off = align_up(off + 4 * Hq * units * (blk * d + 2 * blk));
   L->total_bytes = off;
   return FP_OK;
 }
@@ -157,6 +180,10 @@ int run_plan(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   a.total_tokens = p->total_tokens;
   a.nb_sum_cap = L.nb_sum_cap;
   a.block = p->block_size;
+  a.last_n = p->last_n_block;
+  a.split_blocks = L.split_blocks;
+  a.units = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + L.units_off);
+  a.unit_cap = L.unit_cap;
   const hipError_t e = fp::launch_plan(a, s);
   return e == hipSuccess ? FP_OK : hip_fail(e, "plan launch");
 }
@@ -243,11 +270,19 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   a.Hq = p->num_q_heads;
   a.Hkv = p->num_kv_heads;
   a.sm_scale_log2 = sm_scale_log2(p->head_dim);
-  const int64_t grid = fp::attn_grid(p->num_q_heads, p->num_kv_heads, L.nb_sum_cap);
-  const hipError_t e =
-      p->dtype == FP_DTYPE_F32
-          ? fp::launch_attn_f32(a, p->head_dim, p->block_size, grid, s)
-          : fp::launch_attn(a, p->dtype, p->head_dim, p->block_size, grid, s);
+  a.last_n = p->last_n_block;
+  a.split_blocks = L.split_blocks;
+  a.units = reinterpret_cast<const int32_t*>(base + L.units_off);
+  a.part = reinterpret_cast<float*>(base + L.part_off);
+  a.unit_cap = L.unit_cap;
+  a.unit_slots = (static_cast<int64_t>(p->num_q_heads) * L.unit_cap + 7) / 8 * 8;
+  const int64_t grid =
+      a.unit_slots + fp::attn_grid(p->num_q_heads, p->num_kv_heads, L.nb_sum_cap);
+  hipError_t e = p->dtype == FP_DTYPE_F32
+                     ? fp::launch_attn_f32(a, p->head_dim, p->block_size, grid, s)
+                     : fp::launch_attn(a, p->dtype, p->head_dim, p->block_size, grid, s);
+  if (e == hipSuccess && L.split_blocks > 0)
+    e = fp::launch_merge(a, p->dtype, p->head_dim, p->block_size, s);
   return e == hipSuccess ? FP_OK : hip_fail(e, "attention launch");
 }
 
@@ -290,7 +325,7 @@ int scratch_on_current_device(void** out) {
 
 extern "C" {
 
-int fp_abi_version(void) { return 4; }
+int fp_abi_version(void) { return 5; }
 
 const char* fp_last_error(void) { return g_last_error.c_str(); }
 

@@ -167,6 +167,24 @@ struct ItemRec {
   int64_t tri;   // seq_tri[b] + i (i + 1) / 2: start of the item's index list
 };
 
+// One chunk of a split row (48 bytes): the row's item record, the chunk index
+// and the row's chunk count. A split row is a last_n row (every causal block
+// selected, so its list is 0 .. i) of more than split_blocks blocks; chunk c
+// covers list entries c * split_blocks .. min((c + 1) * split_blocks, i + 1) - 1.
+struct UnitRec {
+  ItemRec r;
+  int32_t c, nc;
+  int32_t pad[2];
+};
+
+// The rule shared by the plan (which emits the chunks) and the attention
+// kernel (which leaves such rows to the chunks): row i of a sequence of nb
+// blocks is split when it is one of the last_n rows and has more than
+// split_blocks blocks.
+__device__ __forceinline__ bool row_is_split(int i, int nb, int last_n, int split_blocks) {
+  return split_blocks > 0 && i >= nb - last_n && i + 1 > split_blocks;
+}
+
 // Workspace views shared by all kernels (device pointers into the workspace).
 struct SeqTables {
   uint32_t* status;

@@ -17,6 +17,10 @@ struct PlanArgs {
   int64_t total_tokens;
   int64_t nb_sum_cap;  // workspace capacity of sum_b NB_b (items, counts, pooled K)
   int32_t block;       // tokens per block
+  int32_t last_n;      // last_n_block of the selection
+  int32_t split_blocks;  // blocks per chunk of a split row (0: none)
+  int32_t* units;      // chunk units: count at [0], records from byte 64
+  int64_t unit_cap;
 };
 
 struct PoolArgs {
@@ -63,6 +67,16 @@ struct AttnArgs {
   int64_t nb_sum_cap;
   int32_t B, Hq, Hkv;
   float sm_scale_log2;
+  // split rows: the first unit_slots workgroups run the chunk units (map_item
+  // over num_q_heads x unit_cap, rounded up to a multiple of 8 so that the
+  // row workgroups after them keep their XCD), writing fp32 partials that
+  // k_merge combines
+  int32_t last_n;
+  int32_t split_blocks;
+  const int32_t* units;
+  float* part;
+  int64_t unit_cap;
+  int64_t unit_slots;
 };
 
 struct KvCacheArgs {
@@ -89,6 +103,8 @@ hipError_t launch_search(const SearchArgs& a, int dtype, int head_dim, int block
                          bool from_scores, hipStream_t s);
 hipError_t launch_attn(const AttnArgs& a, int dtype, int head_dim, int block, int64_t grid,
                        hipStream_t s);
+// combines the chunk partials of the split rows into their output rows
+hipError_t launch_merge(const AttnArgs& a, int dtype, int head_dim, int block, hipStream_t s);
 hipError_t launch_attn_f32(const AttnArgs& a, int head_dim, int block, int64_t grid,
                            hipStream_t s);
 

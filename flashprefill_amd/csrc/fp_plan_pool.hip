@@ -132,28 +132,57 @@ __global__ __launch_bounds__(1024) void k_plan(PlanArgs a) {
   for (int i = t; i < a.nb_max; i += nt) s_lvl[i] = 0;
   __syncthreads();
 
-  // 2. prefix sums of NB_b and NB_b (NB_b + 1) / 2; level histogram
-  int64_t carry_tile = 0, carry_tri = 0;
+  // 2. prefix sums of NB_b and NB_b (NB_b + 1) / 2; level histogram; the
+  //    chunk units of the split rows (row_is_split), numbered by a prefix sum
+  //    over sequences so that the chunks of one row are consecutive
+  int64_t carry_tile = 0, carry_tri = 0, carry_unit = 0;
+  UnitRec* urec = reinterpret_cast<UnitRec*>(reinterpret_cast<char*>(a.units) + 64);
+  const int C = a.split_blocks;
   for (int base = 0; base < a.B; base += nt) {
     const int b = base + t;
     const int64_t nb = b < a.B ? s_pre[b] : 0;
-    int64_t tot1, tot2;
+    int64_t nu = 0;
+    for (int i = max(static_cast<int>(nb) - a.last_n, 0); i < nb; ++i)
+      if (row_is_split(i, static_cast<int>(nb), a.last_n, C)) nu += (i + C) / C;
+    int64_t tot1, tot2, tot3;
     const int64_t e1 = block_exscan_i64(nb, s_red, &tot1);
     const int64_t e2 = block_exscan_i64(nb * (nb + 1) / 2, s_red, &tot2);
+    const int64_t e3 = block_exscan_i64(nu, s_red, &tot3);
     if (b < a.B) {
       tab.seq_tile[b] = carry_tile + e1;
       tab.seq_tri[b] = carry_tri + e2;
       if (nb > 0) atomicAdd(&s_lvl[nb - 1], 1);
+      int64_t u = carry_unit + e3;
+      for (int i = max(static_cast<int>(nb) - a.last_n, 0); i < nb; ++i) {
+        if (!row_is_split(i, static_cast<int>(nb), a.last_n, C)) continue;
+        const int nc = (i + C) / C;
+        for (int c = 0; c < nc; ++c, ++u) {
+          if (u >= a.unit_cap) continue;  // the host bound makes this unreachable
+          UnitRec ur;
+          ur.r.b = b;
+          ur.r.i = i;
+          ur.r.L = tab.seq_len[b];
+          ur.r.tile = static_cast<int32_t>(carry_tile + e1 + i);
+          ur.r.t0 = tab.seq_start[b];
+          ur.r.tri = carry_tri + e2 + static_cast<int64_t>(i) * (i + 1) / 2;
+          ur.c = c;
+          ur.nc = nc;
+          ur.pad[0] = ur.pad[1] = 0;
+          urec[u] = ur;
+        }
+      }
     }
     __syncthreads();  // all reads of s_pre[b] in this chunk are done
     if (b < a.B) s_pre[b] = static_cast<int32_t>(carry_tile + e1);
     carry_tile += tot1;
     carry_tri += tot2;
+    carry_unit += tot3;
   }
   if (t == 0) {
     tab.seq_tile[a.B] = carry_tile;
     tab.seq_tri[a.B] = carry_tri;
     s_pre[a.B] = static_cast<int32_t>(carry_tile);
+    a.units[0] = static_cast<int32_t>(min(carry_unit, a.unit_cap));
   }
   __syncthreads();
 
@@ -196,10 +225,18 @@ __global__ __launch_bounds__(1024) void k_plan(PlanArgs a) {
   if (t == 0) *tab.status = s_status;
 }
 
+// One workgroup per (key block g, kv head hh): 256 threads = R row groups x
+// D / 8 chunks of 16 bytes; each thread sums its rows of one chunk in fp32,
+// the R partial sums are added through LDS in row-group order and the mean is
+// rounded once. Several workgroups per block keep short sequences from
+// running on a handful of CUs.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void k_pool(PoolArgs a) {
+  constexpr int C = D / 8;    // 16-byte chunks per head row
+  constexpr int R = 256 / C;  // row groups
   __shared__ float red[256 * 8];
-  const int64_t g = blockIdx.x;
+  const int64_t g = blockIdx.x / a.Hkv;
+  const int hh = static_cast<int>(blockIdx.x % a.Hkv);
   const int64_t nsum = a.tab.seq_tile[a.B];
   if (g >= nsum) return;
   const int b = find_seq(a.tab.seq_tile, a.B, g);
@@ -207,65 +244,39 @@ __global__ __launch_bounds__(256) void k_pool(PoolArgs a) {
   const int L = a.tab.seq_len[b];
   const int64_t t0 = a.tab.seq_start[b] + static_cast<int64_t>(i) * a.block;
   const int rows = min(a.block, L - i * a.block);
-  constexpr int CPH = D / 8;                 // 16-byte chunks per head row
-  const int C = a.Hkv * CPH;                 // chunks per token row (all kv heads)
-  const int t = threadIdx.x;
+  const int t = threadIdx.x, c = t % C, rg = t / C;
   const float inv = 1.0f / static_cast<float>(rows);
-  uint16_t* out = a.mk + g * static_cast<int64_t>(a.Hkv) * D;
-
-  if (C <= 256) {
-    const int R = 256 / C;  // row groups reduced through LDS
-    const int c = t % C, rg = t / C;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (rg < R) {
-      const int hh = c / CPH, x0 = (c % CPH) * 8;
-      const uint16_t* src = a.k + t0 * a.kst + hh * a.khs + x0;
-      for (int r = rg; r < rows; r += R) {
-        const uint4 v = ld16(src + static_cast<int64_t>(r) * a.kst);
-        const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
+  const uint16_t* src = a.k + t0 * a.kst + hh * a.khs + c * 8;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int r = rg; r < rows; r += R) {
+    const uint4 v = ld16(src + static_cast<int64_t>(r) * a.kst);
+    const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) acc[q] += T::to_f32(e[q]);
-      }
+    for (int q = 0; q < 8; ++q) acc[q] += T::to_f32(e[q]);
+  }
 #pragma unroll
-      for (int q = 0; q < 8; ++q) red[(rg * C + c) * 8 + q] = acc[q];
+  for (int q = 0; q < 8; ++q) red[t * 8 + q] = acc[q];
+  __syncthreads();
+  if (rg == 0) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      float s = 0.f;
+      for (int r = 0; r < R; ++r) s += red[(r * C + c) * 8 + q];
+      acc[q] = s;
     }
-    __syncthreads();
-    if (rg == 0) {
+    uint16_t o[8];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        float s = 0.f;
-        for (int r = 0; r < R; ++r) s += red[(r * C + c) * 8 + q];
-        acc[q] = s;
-      }
-      uint16_t o[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) o[q] = T::from_f32(acc[q] * inv);
-      st16(out + c * 8, *reinterpret_cast<const uint4*>(o));
-    }
-  } else {
-    for (int c = t; c < C; c += 256) {
-      const int hh = c / CPH, x0 = (c % CPH) * 8;
-      const uint16_t* src = a.k + t0 * a.kst + hh * a.khs + x0;
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int r = 0; r < rows; ++r) {
-        const uint4 v = ld16(src + static_cast<int64_t>(r) * a.kst);
-        const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) acc[q] += T::to_f32(e[q]);
-      }
-      uint16_t o[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) o[q] = T::from_f32(acc[q] * inv);
-      st16(out + c * 8, *reinterpret_cast<const uint4*>(o));
-    }
+    for (int q = 0; q < 8; ++q) o[q] = T::from_f32(acc[q] * inv);
+    uint16_t* out = a.mk + (g * a.Hkv + hh) * static_cast<int64_t>(D) + c * 8;
+    st16(out, *reinterpret_cast<const uint4*>(o));
   }
 }
 
 // fp32 keys: the block mean summed in fp64 (in row order) and rounded once to
-// fp32, one thread per (kv head, dim) element of the block (consecutive
-// threads read consecutive addresses of a row).
+// fp32, one thread per dim of one (key block, kv head) per workgroup.
 __global__ __launch_bounds__(256) void k_pool_f32(PoolArgs a, int head_dim) {
-  const int64_t g = blockIdx.x;
+  const int64_t g = blockIdx.x / a.Hkv;
+  const int hh = static_cast<int>(blockIdx.x % a.Hkv);
   const int64_t nsum = a.tab.seq_tile[a.B];
   if (g >= nsum) return;
   const int b = find_seq(a.tab.seq_tile, a.B, g);
@@ -274,13 +285,12 @@ __global__ __launch_bounds__(256) void k_pool_f32(PoolArgs a, int head_dim) {
   const int64_t t0 = a.tab.seq_start[b] + static_cast<int64_t>(i) * a.block;
   const int rows = min(a.block, L - i * a.block);
   const float* k = reinterpret_cast<const float*>(a.k);
-  float* out = reinterpret_cast<float*>(a.mk) + g * static_cast<int64_t>(a.Hkv) * head_dim;
-  for (int e = threadIdx.x; e < a.Hkv * head_dim; e += blockDim.x) {
-    const int hh = e / head_dim, x = e % head_dim;
+  float* out = reinterpret_cast<float*>(a.mk) + (g * a.Hkv + hh) * static_cast<int64_t>(head_dim);
+  for (int x = threadIdx.x; x < head_dim; x += blockDim.x) {
     const float* src = k + t0 * a.kst + hh * a.khs + x;
     double sum = 0.0;
     for (int r = 0; r < rows; ++r) sum += static_cast<double>(src[static_cast<int64_t>(r) * a.kst]);
-    out[e] = static_cast<float>(sum / static_cast<double>(rows));
+    out[x] = static_cast<float>(sum / static_cast<double>(rows));
   }
 }
 
@@ -294,7 +304,8 @@ hipError_t launch_plan(const PlanArgs& a, hipStream_t s) {
 
 hipError_t launch_pool(const PoolArgs& a, int dtype, int head_dim, int64_t grid, hipStream_t s) {
   if (grid <= 0) return hipSuccess;
-  const dim3 g(static_cast<unsigned>(grid)), blk(256);
+  // one workgroup per (key block, kv head)
+  const dim3 g(static_cast<unsigned>(grid * a.Hkv)), blk(256);
   if (dtype == FP_DTYPE_F32) {
     hipLaunchKernelGGL(k_pool_f32, g, blk, 0, s, a, head_dim);
   } else if (dtype == FP_DTYPE_BF16) {

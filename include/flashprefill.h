@@ -115,9 +115,15 @@ typedef struct fp_ws_layout {
     size_t rowrec_off;   /* int32[Hq * nb_sum_cap][4] by (head, item): count, first and
                             second list entry, diagonal block kept */
     size_t idx_off;
+    size_t units_off;    /* split rows (16-bit inputs): int32 count at +0, then from +64
+                            records of 48 bytes: the row's item record, chunk, chunks */
+    size_t part_off;     /* fp32 partial results of the chunks, per (head, unit):
+                            acc[block][head_dim], m[block], l[block] */
     int64_t nb_sum_cap;  /* >= sum_b NB_b */
     int64_t tri_cap;     /* >= sum_b NB_b (NB_b + 1) / 2 */
+    int64_t unit_cap;    /* >= number of chunk units (0: no row is split) */
     int32_t nb_max;      /* ceil(max_seq_len / block_size) */
+    int32_t split_blocks; /* blocks per chunk of a split row (0: no row is split) */
 } fp_ws_layout;
 
 /* Validate `p` and compute the workspace layout (no device work). */
@@ -153,7 +159,7 @@ int fp_sparse_attn_fwd(const fp_problem* p, void* workspace, void* stream);
  * static array and are not readable through fp_read_status. Calls no
  * hipMalloc / hipFree; the first call on a device reads the array's device
  * address once (hipGetSymbolAddress). */
-#define FP_NOALLOC_SCRATCH_BYTES (80u * 1024u * 1024u)
+#define FP_NOALLOC_SCRATCH_BYTES (96u * 1024u * 1024u)
 int fp_flashprefill_noalloc(const fp_problem* p, void* stream);
 
 /* Paged KV-cache write of the vLLM backend hook: for every token t < num_tokens

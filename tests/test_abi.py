@@ -63,10 +63,33 @@ def test_layout_bounds():
     cap = L.nb_sum_cap
     assert L.tri_cap == (cap // 32) * 32 * 33 // 2 + (cap % 32) * (cap % 32 + 1) // 2
     offs = [L.status_off, L.seq_tile_off, L.seq_tri_off, L.seq_start_off, L.seq_len_off,
-            L.items_off, L.mk_off, L.cnt_off, L.rowrec_off, L.idx_off]
+            L.items_off, L.mk_off, L.cnt_off, L.rowrec_off, L.idx_off, L.units_off,
+            L.part_off]
     assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
-    assert L.total_bytes >= L.idx_off + 4 * 8 * L.tri_cap
+    assert L.units_off >= L.idx_off + 4 * 8 * L.tri_cap
+    assert L.total_bytes >= L.part_off + 4 * 8 * L.unit_cap * (128 * 128 + 2 * 128)
     assert _lib.load().fp_workspace_bytes(ctypes.byref(_problem())) == L.total_bytes
+
+
+def test_split_row_policy():
+    # last_n rows select every causal block; rows longer than C = max(8, ceil(NB / 4))
+    # blocks run as chunks of C (at most 4 per row) on 16-bit inputs
+    rc, L = _layout(_problem())  # 3 sequences, NB <= 32: C = 8, 3 x 2 rows x 4 chunks
+    assert rc == _lib.FP_OK and L.split_blocks == 8 and L.unit_cap == 24
+    S = 131072
+    one = dict(batch=1, max_seq_len=S, total_tokens=S, num_q_heads=32, num_kv_heads=8,
+               q_stride_tok=32 * 128, k_stride_tok=8 * 128, v_stride_tok=8 * 128,
+               o_stride_tok=32 * 128)
+    rc, L = _layout(_problem(**one))
+    assert rc == _lib.FP_OK and L.split_blocks == 256 and L.unit_cap == 2 * 4
+    for off in (dict(dtype=_lib.FP_DTYPE_F32), dict(last_n_block=0),
+                dict(max_seq_len=1024, total_tokens=3 * 1024)):  # fp32, no dense rows, NB <= 8
+        rc, L = _layout(_problem(**off))
+        assert rc == _lib.FP_OK and L.split_blocks == 0 and L.unit_cap == 0
+    # many long sequences: every row's share is small anyway, so no split
+    rc, L = _layout(_problem(batch=512, max_seq_len=8192, total_tokens=512 * 8192,
+                             num_q_heads=32))
+    assert rc == _lib.FP_OK and L.split_blocks == 0
 
 
 def test_layout_bounds_block_64():
