@@ -92,6 +92,33 @@ def test_split_row_policy():
     assert rc == _lib.FP_OK and L.split_blocks == 0
 
 
+def test_split_units_never_exceed_the_capacity():
+    # restatement of the plan kernel's chunk emission (fp_plan_pool.hip, pass 2) on
+    # random ragged batches: the units it writes stay within the host's unit_cap
+    import random
+    rnd = random.Random(5)
+    for trial in range(300):
+        B = rnd.choice([1, 2, 3, 5, 17])
+        block = rnd.choice([64, 128])
+        max_len = rnd.choice([700, 2048, 5000, 20000])
+        lens = [rnd.randint(0, max_len) for _ in range(B)]
+        lens[0] = max_len
+        last_n = rnd.choice([1, 2, 3, 7])
+        T = sum(lens) + rnd.randint(0, 300)
+        rc, L = _layout(_problem(batch=B, max_seq_len=max_len, total_tokens=T,
+                                 block_size=block, last_n_block=last_n))
+        assert rc == _lib.FP_OK
+        C = L.split_blocks
+        n = 0
+        for Ls in lens:
+            nb = -(-Ls // block)
+            for i in range(max(nb - last_n, 0), nb):
+                if C > 0 and i + 1 > C:
+                    assert -(-(i + 1) // C) <= 4  # the merge kernel combines at most 4
+                    n += -(-(i + 1) // C)
+        assert n <= L.unit_cap, (lens, block, last_n, C, n, L.unit_cap)
+
+
 def test_layout_bounds_block_64():
     rc, L = _layout(_problem(block_size=64))
     assert rc == _lib.FP_OK
