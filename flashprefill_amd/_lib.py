@@ -30,7 +30,7 @@ ABI_VERSION = 5
 EXPORTS = (
     "fp_workspace_layout", "fp_workspace_bytes", "fp_flashprefill", "fp_plan", "fp_pool_k",
     "fp_search", "fp_select", "fp_sparse_attn_fwd", "fp_read_status", "fp_last_error",
-    "fp_abi_version", "fp_flashprefill_noalloc", "fp_kv_cache_write",
+    "fp_abi_version", "fp_flashprefill_noalloc", "fp_kv_cache_write", "fp_rope_qk",
 )
 NOALLOC_SCRATCH_BYTES = 96 * 1024 * 1024
 
@@ -69,6 +69,19 @@ class FpWsLayout(ctypes.Structure):
         ("nb_sum_cap", ctypes.c_int64), ("tri_cap", ctypes.c_int64),
         ("unit_cap", ctypes.c_int64),
         ("nb_max", ctypes.c_int32), ("split_blocks", ctypes.c_int32),
+    ]
+
+
+class FpRopeArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("q_stride_tok", ctypes.c_int64), ("q_stride_head", ctypes.c_int64),
+        ("k", ctypes.c_void_p), ("k_stride_tok", ctypes.c_int64), ("k_stride_head", ctypes.c_int64),
+        ("positions", ctypes.c_void_p), ("num_tokens", ctypes.c_int64),
+        ("cos_table", ctypes.c_void_p), ("sin_table", ctypes.c_void_p),
+        ("num_positions", ctypes.c_int64),
+        ("q_norm", ctypes.c_void_p), ("k_norm", ctypes.c_void_p), ("eps", ctypes.c_float),
+        ("num_q_heads", ctypes.c_int32), ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32), ("dtype", ctypes.c_int32),
     ]
 
 
@@ -112,6 +125,7 @@ def load(path: Path = LIB_PATH) -> ctypes.CDLL:
         getattr(lib, name).argtypes = [P, vp, vp]
     lib.fp_flashprefill_noalloc.argtypes = [P, vp]
     lib.fp_kv_cache_write.argtypes = [ctypes.POINTER(FpKvCacheArgs), vp]
+    lib.fp_rope_qk.argtypes = [ctypes.POINTER(FpRopeArgs), vp]
     lib.fp_search.argtypes = [P, vp, vp, vp, vp]
     lib.fp_select.argtypes = [P, vp, vp, vp, vp]
     lib.fp_read_status.argtypes = [P, vp, vp, ctypes.POINTER(ctypes.c_uint32)]

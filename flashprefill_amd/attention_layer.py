@@ -9,15 +9,21 @@ with q_norm / k_norm), written as one module over packed varlen tokens
 (patches/patch_loader_vllm_0_12_0.py:187-199). Q, K and V are views into one
 fused QKV projection (the op takes strided inputs; no copies), RoPE uses the
 rotate-half convention with per-sequence positions taken from ``cu_seqlens``.
-The projections are plain library GEMMs (torch -> hipBLASLt).
+The projections are plain library GEMMs (torch -> hipBLASLt). On the GPU
+the q/k RMSNorm and RoPE run as one HIP kernel in place on the projection
+(``fp_rope_qk``; the torch functions below are its reference and produce the
+same bits).
 """
 
 from __future__ import annotations
 
 from typing import Optional, Tuple
 
+import ctypes
+
 import torch
 
+from . import _lib
 from .flashprefill_varlen_func import flash_prefill_varlen_func
 
 
@@ -48,6 +54,49 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
     xf = x.float()
     rot = torch.cat([-xf[..., d // 2:], xf[..., :d // 2]], dim=-1)
     return (xf * cos.unsqueeze(1) + rot * sin.unsqueeze(1)).to(x.dtype)
+
+
+_TABLES = {}
+
+
+def rope_position_tables(num_positions: int, head_dim: int, theta: float, device
+                         ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """cos / sin per position (num_positions, head_dim / 2), fp32 from fp64
+    angles (the values rope_tables repeats for both halves), cached per
+    (size, head_dim, theta, device); grown to the next power of two."""
+    n = 1 << max(int(num_positions) - 1, 1).bit_length()
+    key = (head_dim, float(theta), str(torch.device(device)))
+    hit = _TABLES.get(key)
+    if hit is None or hit[0].shape[0] < n:
+        pos = torch.arange(n, device=device, dtype=torch.float64)
+        inv = theta ** (-torch.arange(0, head_dim, 2, device=device, dtype=torch.float64) / head_dim)
+        ang = pos.view(-1, 1) * inv.view(1, -1)
+        hit = (ang.cos().float().contiguous(), ang.sin().float().contiguous())
+        _TABLES[key] = hit
+    return hit
+
+
+def fused_rope_qk(q: torch.Tensor, k: torch.Tensor, positions: torch.Tensor, theta: float,
+                  q_norm: Optional[torch.Tensor] = None, k_norm: Optional[torch.Tensor] = None,
+                  eps: float = 1e-6, max_position: Optional[int] = None) -> None:
+    """RMSNorm (when the weights are given) and RoPE of q (T, Hq, d) and k
+    (T, Hkv, d) in place with the HIP kernel (bf16 / fp16 on the GPU; no
+    fallback). ``positions`` (T,) int64 on the same device."""
+    T, Hq, d = q.shape
+    n = int(max_position) if max_position is not None else int(positions.max().item()) + 1
+    cos, sin = rope_position_tables(max(n, 1), d, theta, q.device)
+    a = _lib.FpRopeArgs()
+    a.q, a.q_stride_tok, a.q_stride_head = q.data_ptr(), q.stride(0), q.stride(1)
+    a.k, a.k_stride_tok, a.k_stride_head = k.data_ptr(), k.stride(0), k.stride(1)
+    a.positions, a.num_tokens = positions.data_ptr(), T
+    a.cos_table, a.sin_table, a.num_positions = cos.data_ptr(), sin.data_ptr(), cos.shape[0]
+    a.q_norm = q_norm.data_ptr() if q_norm is not None else None
+    a.k_norm = k_norm.data_ptr() if k_norm is not None else None
+    a.eps = eps
+    a.num_q_heads, a.num_kv_heads, a.head_dim = Hq, k.shape[1], d
+    a.dtype = {torch.bfloat16: _lib.FP_DTYPE_BF16, torch.float16: _lib.FP_DTYPE_F16}[q.dtype]
+    _lib.check(_lib.load().fp_rope_qk(ctypes.byref(a),
+                                      torch.cuda.current_stream(q.device).cuda_stream))
 
 
 def rms_norm_heads(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
@@ -92,10 +141,23 @@ class PrefillAttention(torch.nn.Module):
         q = qkv[:, :self.Hq]
         k = qkv[:, self.Hq:self.Hq + self.Hkv]
         v = qkv[:, self.Hq + self.Hkv:]
+        pos = positions_from_cu_seqlens(cu_seqlens, T)
+        if qkv.is_cuda and qkv.dtype in (torch.bfloat16, torch.float16):
+            # one kernel, in place on the projection (q and k stay views of it)
+            fused_rope_qk(q, k, pos, self.rope_theta,
+                          self.q_norm if self.qk_norm else None,
+                          self.k_norm if self.qk_norm else None, self.rms_eps,
+                          max_position=T)
+            return q, k, v
+        return self.project_qkv_reference(q, k, v, pos)
+
+    def project_qkv_reference(self, q, k, v, pos):
+        """The torch composition of the same steps (the fused kernel's
+        reference): RMSNorm rounded to the input dtype, then RoPE."""
         if self.qk_norm:
             q = rms_norm_heads(q, self.q_norm, self.rms_eps)
             k = rms_norm_heads(k, self.k_norm, self.rms_eps)
-        cos, sin = rope_tables(positions_from_cu_seqlens(cu_seqlens, T), self.d, self.rope_theta)
+        cos, sin = rope_tables(pos, self.d, self.rope_theta)
         return apply_rope(q, cos, sin), apply_rope(k, cos, sin), v
 
     def forward(self, x: torch.Tensor, cu_seqlens: torch.Tensor, max_seq_len: int

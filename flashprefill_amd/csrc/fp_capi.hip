@@ -408,6 +408,47 @@ int fp_flashprefill_noalloc(const fp_problem* p, void* stream) {
   return run_attn(p, L, ws, s);
 }
 
+int fp_rope_qk(const fp_rope_args* a, void* stream) {
+  if (!a) return fail(FP_E_INVALID_ARG, "rope args are NULL");
+  if (a->dtype != FP_DTYPE_BF16 && a->dtype != FP_DTYPE_F16)
+    return fail(FP_E_UNSUPPORTED, "rope: dtype %d unsupported (bf16 or fp16)", a->dtype);
+  if (a->head_dim != 64 && a->head_dim != 128)
+    return fail(FP_E_UNSUPPORTED, "rope: head_dim %d unsupported (64 or 128)", a->head_dim);
+  if (a->num_tokens < 0 || a->num_q_heads < 0 || a->num_kv_heads < 0 || a->num_positions < 1)
+    return fail(FP_E_INVALID_ARG, "rope: negative sizes or an empty table");
+  if (a->num_tokens == 0) return FP_OK;
+  if ((a->num_q_heads > 0 && !a->q) || (a->num_kv_heads > 0 && !a->k) || !a->positions ||
+      !a->cos_table || !a->sin_table)
+    return fail(FP_E_INVALID_ARG, "rope: NULL pointer");
+  const int64_t st[4] = {a->q_stride_tok, a->q_stride_head, a->k_stride_tok, a->k_stride_head};
+  for (int i = 0; i < 4; ++i)
+    if (st[i] < 0 || st[i] % 8)
+      return fail(FP_E_INVALID_ARG, "rope: strides must be non-negative multiples of 8 elements");
+  if ((a->q && !aligned16(a->q)) || (a->k && !aligned16(a->k)) || !aligned16(a->cos_table) ||
+      !aligned16(a->sin_table))
+    return fail(FP_E_INVALID_ARG, "rope: q / k / tables must be 16-byte aligned");
+  fp::RopeArgs r;
+  r.q = a->q;
+  r.q_stride_tok = a->q_stride_tok;
+  r.q_stride_head = a->q_stride_head;
+  r.k = a->k;
+  r.k_stride_tok = a->k_stride_tok;
+  r.k_stride_head = a->k_stride_head;
+  r.num_q_heads = a->num_q_heads;
+  r.num_kv_heads = a->num_kv_heads;
+  r.head_dim = a->head_dim;
+  r.positions = a->positions;
+  r.num_tokens = a->num_tokens;
+  r.cos_tab = a->cos_table;
+  r.sin_tab = a->sin_table;
+  r.num_positions = a->num_positions;
+  r.q_norm = a->q_norm;
+  r.k_norm = a->k_norm;
+  r.eps = a->eps;
+  const hipError_t e = fp::launch_rope(r, a->dtype, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? FP_OK : hip_fail(e, "rope launch");
+}
+
 int fp_kv_cache_write(const fp_kv_cache_args* a, void* stream) {
   if (!a) return fail(FP_E_INVALID_ARG, "kv-cache arguments are NULL");
   if (a->dtype != FP_DTYPE_BF16 && a->dtype != FP_DTYPE_F16)

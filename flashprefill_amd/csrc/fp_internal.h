@@ -96,7 +96,24 @@ struct KvCacheArgs {
   int32_t elem_bytes;
 };
 
+struct RopeArgs {
+  void* q;
+  int64_t q_stride_tok, q_stride_head;
+  void* k;
+  int64_t k_stride_tok, k_stride_head;
+  int32_t num_q_heads, num_kv_heads, head_dim;
+  const int64_t* positions;  // per token
+  int64_t num_tokens;
+  const float* cos_tab;      // (num_positions, head_dim / 2)
+  const float* sin_tab;
+  int64_t num_positions;
+  const void* q_norm;        // nullable: head_dim weights in the input dtype
+  const void* k_norm;
+  float eps;
+};
+
 hipError_t launch_plan(const PlanArgs& a, hipStream_t s);
+hipError_t launch_rope(const RopeArgs& a, int dtype, hipStream_t s);
 hipError_t launch_kv_cache_write(const KvCacheArgs& a, hipStream_t s);
 hipError_t launch_pool(const PoolArgs& a, int dtype, int head_dim, int64_t grid, hipStream_t s);
 hipError_t launch_search(const SearchArgs& a, int dtype, int head_dim, int block, int64_t grid,

@@ -187,6 +187,38 @@ typedef struct fp_kv_cache_args {
 } fp_kv_cache_args;
 int fp_kv_cache_write(const fp_kv_cache_args* a, void* stream);
 
+/* Rotary position embedding (rotate-half) with optional per-head RMSNorm, in
+ * place on the query and key heads of a decoder-layer attention block. No
+ * kernel of the reference does this: it replaces the torch steps its model
+ * callers run before the op (ruler/models/llama.py:293-301 apply_rotary_pos_emb,
+ * ruler/models/qwen3.py:171-176 q_norm / k_norm then RoPE). For every token t
+ * and head h of q (num_q_heads) and k (num_kv_heads):
+ *   x <- round(x * rsqrt(mean(x^2) + eps) * norm)   when the head's norm is set
+ *   x[j]       <- round(x[j] * cos[p][j] - x[j + d/2] * sin[p][j])
+ *   x[j + d/2] <- round(x[j + d/2] * cos[p][j] + x[j] * sin[p][j]),  j < d/2,
+ * p = positions[t] (clamped to the table), fp32 math, each product and sum
+ * rounded on its own (the bits of the torch composition of the same steps).
+ * Strides in elements (multiples of 8), head dim contiguous. */
+typedef struct fp_rope_args {
+    void* q;                  /* (tokens, num_q_heads, head_dim), updated in place */
+    int64_t q_stride_tok, q_stride_head;
+    void* k;                  /* (tokens, num_kv_heads, head_dim), updated in place */
+    int64_t k_stride_tok, k_stride_head;
+    const int64_t* positions; /* device, num_tokens entries */
+    int64_t num_tokens;
+    const float* cos_table;   /* device fp32 (num_positions, head_dim / 2) */
+    const float* sin_table;
+    int64_t num_positions;
+    const void* q_norm;       /* nullable: head_dim weights in the input dtype */
+    const void* k_norm;
+    float eps;
+    int32_t num_q_heads;
+    int32_t num_kv_heads;
+    int32_t head_dim;         /* 64 or 128 */
+    int32_t dtype;            /* FP_DTYPE_BF16 or FP_DTYPE_F16 */
+} fp_rope_args;
+int fp_rope_qk(const fp_rope_args* a, void* stream);
+
 /* Copy the device status word to the host (synchronises `stream`). */
 int fp_read_status(const fp_problem* p, void* workspace, void* stream, uint32_t* status);
 

@@ -92,6 +92,26 @@ def test_split_row_policy():
     assert rc == _lib.FP_OK and L.split_blocks == 0
 
 
+@pytest.mark.parametrize("field,value,code", [
+    ("dtype", _lib.FP_DTYPE_F32, _lib.FP_E_UNSUPPORTED),
+    ("head_dim", 96, _lib.FP_E_UNSUPPORTED),
+    ("q_stride_tok", 100, _lib.FP_E_INVALID_ARG),
+    ("num_positions", 0, _lib.FP_E_INVALID_ARG),
+    ("positions", None, _lib.FP_E_INVALID_ARG),
+])
+def test_rope_arguments_rejected_on_host(field, value, code):
+    a = _lib.FpRopeArgs()
+    a.q = a.k = a.positions = a.cos_table = a.sin_table = 0x10000
+    a.q_stride_tok, a.q_stride_head = 12 * 128, 128
+    a.k_stride_tok, a.k_stride_head = 12 * 128, 128
+    a.num_tokens, a.num_positions = 5, 8
+    a.num_q_heads, a.num_kv_heads, a.head_dim, a.dtype = 8, 2, 128, _lib.FP_DTYPE_BF16
+    setattr(a, field, value)
+    lib = _lib.load()
+    assert lib.fp_rope_qk(ctypes.byref(a), None) == code
+    assert lib.fp_last_error()
+
+
 def test_split_units_never_exceed_the_capacity():
     # restatement of the plan kernel's chunk emission (fp_plan_pool.hip, pass 2) on
     # random ragged batches: the units it writes stay within the host's unit_cap
