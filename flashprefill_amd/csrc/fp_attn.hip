@@ -33,8 +33,9 @@
 // P is rounded to the input dtype before P.V, the diagonal block masks
 // key > query, and O = acc * (1/l). Two deliberate differences, both at
 // rounding level: m is the max of conditional rescaling (it moves only when a
-// block's max exceeds it by more than kRescaleSlack, so P <= 2^8), and l adds
-// the rounded P (v_dot2c, two scores per instruction) instead of the fp32 p.
+// lane's partial row sum of P against it would exceed kRescaleSum, so P <= 2^8),
+// and l adds the rounded P (v_dot2c, two scores per instruction) instead of the
+// fp32 p.
 #include "fp_attn_common.h"
 
 namespace fp {
@@ -46,10 +47,29 @@ struct AttnState {
   float l_part;
 };
 
-// One selected block: S = K.Q^T, online softmax, O += V^T.P^T, and the
-// pipelined refills of the K / V buffers with block `jn` (when jn >= 0). The
-// list entry at `pf` (the block after jn, or any valid entry) is read into
-// `jpf` right after the K refill is issued, unclamped: the scalar load then
+// P = exp2(s * c - m) of the lane's KT x 16 scores, rounded to the input type
+// in pairs (the B operands of P.V); returns the sum of the rounded values
+template <typename T, int KT>
+__device__ __forceinline__ float exp_pack(const f32x16 (&s)[KT], float m, float c,
+                                          uint32_t (&pk)[KT][8]) {
+  float psum[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int t4 = 0; t4 < KT; ++t4)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(s[t4][2 * e], c, -m));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(s[t4][2 * e + 1], c, -m));
+      pk[t4][e] = pack2<T>(p0, p1);
+      psum[e & 1] = add_pair<T>(pk[t4][e], psum[e & 1]);
+    }
+  return psum[0] + psum[1];
+}
+
+// One selected block (`first`: the row's first, wave-uniform): S = K.Q^T,
+// online softmax, O += V^T.P^T, and the pipelined refills of the K / V
+// buffers with block `jn` (when jn >= 0). The list entry at `pf` (the block
+// after jn, or any valid entry) is read into `jpf` right after the K refill is
+// issued, unclamped: the scalar load then
 // completes behind the softmax, which reads no LDS, instead of stalling the
 // next block (scalar loads share the LDS wait counter, so the compiler waits
 // for them at the first LDS read after them).
@@ -61,7 +81,7 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
                                            const TileLanes<D, BLK, BLK / 32>& tk,
                                            const TileLanes<D, BLK, BLK / 32>& tv,
                                            int jn, const int32_t* pf, int& jpf, int L, float c,
-                                           int w, int lane) {
+                                           bool first, int w, int lane) {
   constexpr int CH = D / 8;
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
@@ -97,16 +117,27 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
         if (key > qrow) s[t4][v] = -INFINITY;
       }
   }
-  float mx = -INFINITY;
+  // P rounded to the input type, packed as the B operands of P.V, is first
+  // formed against the running max; l adds the rounded P that P.V consumes.
+  // The block is taken again with a moved max (and O, l rescaled) only when
+  // some lane's partial row sum exceeds kRescaleSum (every P <= that sum, so
+  // P <= 2^8 on the kept path) or is not finite, and always on the row's first
+  // block, where m is -inf. The block maximum is then computed only on that
+  // path instead of for every block.
+  uint32_t pk[KT][8];
+  float ps = 0.0f;
+  bool move = first;
+  if (!first) {
+    ps = exp_pack<T, KT>(s, st.m_run, c, pk);
+    move = __ballot(!(ps <= kRescaleSum)) != 0;
+  }
+  if (move) {
+    float mx = -INFINITY;
 #pragma unroll
-  for (int t4 = 0; t4 < KT; ++t4)
+    for (int t4 = 0; t4 < KT; ++t4)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[t4][v]);
-  const float m_tile = pair32_max(mx) * c;
-  // the running max moves (and O, l are rescaled) only when some row of the
-  // wave exceeds it by more than kRescaleSlack; always on the row's first block
-  if (__ballot(m_tile > st.m_run + kRescaleSlack)) {
-    const float m_new = fmaxf(st.m_run, m_tile);
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[t4][v]);
+    const float m_new = fmaxf(st.m_run, pair32_max(mx) * c);
     float alpha = __builtin_amdgcn_exp2f(st.m_run - m_new);
     if (alpha != alpha) alpha = 1.0f;
     st.l_part *= alpha;
@@ -115,21 +146,9 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int v = 0; v < 16; ++v) st.o[dt][v] *= alpha;
+    ps = exp_pack<T, KT>(s, st.m_run, c, pk);
   }
-  // P rounded to the input type, packed as the B operands of P.V; l adds the
-  // rounded P that P.V consumes
-  uint32_t pk[KT][8];
-  float psum[2] = {0.0f, 0.0f};
-#pragma unroll
-  for (int t4 = 0; t4 < KT; ++t4)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float p0 = __builtin_amdgcn_exp2f(fmaf(s[t4][2 * e], c, -st.m_run));
-      const float p1 = __builtin_amdgcn_exp2f(fmaf(s[t4][2 * e + 1], c, -st.m_run));
-      pk[t4][e] = pack2<T>(p0, p1);
-      psum[e & 1] = add_pair<T>(pk[t4][e], psum[e & 1]);
-    }
-  st.l_part += psum[0] + psum[1];
+  st.l_part += ps;
 
   if (jn >= 0) vm_barrier<NI>(); else vm_barrier<0>();  // V of this block has landed
   // O^T += V^T . P^T over BLK / 16 steps of 16 keys. B element e of lane (q, half)
@@ -291,12 +310,12 @@ __global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
   for (int n = 0; n < nplain; ++n) {
     const int jn = n + 1 < ncnt ? min(max(jraw, 0), i) : -1;
     attn_block<T, D, BLK, false>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv, jn,
-                            list + min(n + 2, ncnt - 1), jraw, L, c, w, lane);
+                            list + min(n + 2, ncnt - 1), jraw, L, c, n == 0, w, lane);
   }
   if (has_diag) {
     int unused;
     attn_block<T, D, BLK, true>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv, -1,
-                           list, unused, L, c, w, lane);
+                           list, unused, L, c, nplain == 0, w, lane);
   }
 
   const float l = pair32_sum(st.l_part);

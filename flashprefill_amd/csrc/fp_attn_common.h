@@ -71,11 +71,12 @@ __device__ __forceinline__ float add_pair<F16>(uint32_t p, float acc) {
 }
 
 // Conditional rescaling: the running maximum m that P = exp2(s * scale - m)
-// is taken against moves only when a tile's maximum exceeds it by more than
-// this many log2 units, so P <= 2^kRescaleSlack. The output accumulators are
-// rescaled only then (about once per row instead of in most steps). O and l
-// are scaled by the same factors, so O / l is unchanged up to rounding.
-constexpr float kRescaleSlack = 8.0f;
+// is taken against moves only when, against the current m, the sum of a
+// lane's P over one tile would exceed kRescaleSum (so P <= 2^8 on every path),
+// or on a row's first tile. The output accumulators are rescaled only then
+// (about once per row instead of in most steps). O and l are scaled by the
+// same factors, so O / l is unchanged up to rounding.
+constexpr float kRescaleSum = 256.0f;
 
 // wait for this wave's vector-memory ops down to N outstanding, then barrier
 template <int N>
