@@ -355,14 +355,19 @@ def median(xs):
     return xs[len(xs) // 2]
 
 
-def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines, dense_reps=3):
+def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines, dense_reps=3,
+            rounds=1):
     """Time one operator configuration (HIP events on the launch stream):
     the public entry point flash_prefill_varlen_func (its cached workspace
     and argument handling included: what a caller pays per call), the same
     call on a prebuilt descriptor, the plan, search and attention stages,
     density, and the dense baselines (this kernel with every causal block
     selected, torch SDPA flash per sequence with the KV heads expanded;
-    each the median of ``dense_reps`` timings)."""
+    each the median of ``dense_reps`` timings). With ``rounds`` > 1 the
+    public and prebuilt calls are timed alternately that many times (``steps``
+    calls each) and the medians are reported: short configurations otherwise
+    carry the first timed region's ramp-up (their first round runs up to
+    ~10 % slower)."""
     import torch
     from flashprefill_amd import flash_prefill_varlen_func
     from flashprefill_amd.runtime import FlashPrefillCall
@@ -381,8 +386,11 @@ def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines, dense_
         call.run()
     torch.cuda.synchronize()
     print("bench: timing", file=sys.stderr, flush=True)
-    ms_total = timed(public_call, steps)
-    ms_prebuilt = timed(call.run, steps)
+    pub_ms, pre_ms = [], []
+    for _ in range(rounds):
+        pub_ms.append(timed(public_call, steps))
+        pre_ms.append(timed(call.run, steps))
+    ms_total, ms_prebuilt = median(pub_ms), median(pre_ms)
 
     # t_search is pool + score + select, the search of the reference's path
     # (its block-table setup is orchestration); the plan kernel, which builds
@@ -562,7 +570,7 @@ def config_results(config, steps, warmup, dense):
     for spec, alpha, name in config_cases(config):
         print(f"bench: config {config} {name}", file=sys.stderr, flush=True)
         q, k, v, cu = synth.make_inputs(spec, device=dev)
-        r = measure(q, k, v, cu, list(spec.seq_lens), alpha, steps, warmup, dense)
+        r = measure(q, k, v, cu, list(spec.seq_lens), alpha, steps, warmup, dense, rounds=3)
         r.update({"case": name, "seq_lens": list(spec.seq_lens), "num_q_heads": spec.num_q_heads,
                   "num_kv_heads": spec.num_kv_heads, "head_dim": spec.head_dim, "alpha": alpha,
                   "seed": spec.seed})
