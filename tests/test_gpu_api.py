@@ -121,11 +121,16 @@ def test_all_blocks_selected_long_rows():
     _close(o, ref.permute(1, 0, 2).cpu())
 
 
-def test_growing_logits_rescale_every_block():
-    # every key block's logits exceed the previous block's by ~9 log2 units
-    # (more than the kernels' rescaling slack of 8), so the running max moves
-    # and the output accumulators are rescaled on every block; the last
-    # query rows then attend almost only to their own (diagonal) block.
+@pytest.mark.parametrize("step", [70.0, 23.5, 8.0])
+def test_growing_logits_rescale(step):
+    # every key block's logits exceed the previous block's by step / sqrt(d)
+    # * log2(e) log2 units: ~9 (the block maximum alone moves the running max
+    # by more than 2^8 on every block), ~3 (a lane's partial row sum of
+    # P = 2^3-ish values passes 2^8 while no single P does) and ~1 (P grows
+    # past 1 over several blocks before the row sum forces a move), so the
+    # attention kernel's rescale path is taken on every block, on the row-sum
+    # trigger alone, and after runs of blocks kept against a stale maximum.
+    # The last query rows attend almost only to their own (diagonal) block.
     # All blocks selected (alpha 0): dense causal attention vs fp32 SDPA.
     T, Hq, Hkv, d = 2048, 2, 1, 128
     g = torch.Generator().manual_seed(31)
@@ -133,7 +138,7 @@ def test_growing_logits_rescale_every_block():
     e[0] = 1.0
     q = (e + 0.05 * torch.randn(T, Hq, d, generator=g)).to(torch.bfloat16)
     blk = (torch.arange(T) // 128).float()
-    k = (70.0 * blk[:, None, None] * e + torch.randn(T, Hkv, d, generator=g)).to(torch.bfloat16)
+    k = (step * blk[:, None, None] * e + torch.randn(T, Hkv, d, generator=g)).to(torch.bfloat16)
     v = torch.randn(T, Hkv, d, generator=g).to(torch.bfloat16)
     o = torch.empty(T, Hq, d, dtype=torch.bfloat16, device=DEV)
     cu = torch.tensor([0, T], dtype=torch.int32, device=DEV)
