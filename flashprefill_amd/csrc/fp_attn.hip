@@ -48,13 +48,19 @@ struct AttnState {
 };
 
 // P = exp2(s * c - m) of the lane's KT x 16 scores, rounded to the input type
-// in pairs (the B operands of P.V); returns the sum of the rounded values
+// in pairs (the B operands of P.V); returns the sum of the rounded values.
+// Tiles from `live` on (wave-uniform) are entirely masked: P = 0 there.
 template <typename T, int KT>
-__device__ __forceinline__ float exp_pack(const f32x16 (&s)[KT], float m, float c,
+__device__ __forceinline__ float exp_pack(const f32x16 (&s)[KT], float m, float c, int live,
                                           uint32_t (&pk)[KT][8]) {
   float psum[2] = {0.0f, 0.0f};
 #pragma unroll
-  for (int t4 = 0; t4 < KT; ++t4)
+  for (int t4 = 0; t4 < KT; ++t4) {
+    if (t4 >= live) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pk[t4][e] = 0u;
+      continue;
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float p0 = __builtin_amdgcn_exp2f(fmaf(s[t4][2 * e], c, -m));
@@ -62,6 +68,7 @@ __device__ __forceinline__ float exp_pack(const f32x16 (&s)[KT], float m, float 
       pk[t4][e] = pack2<T>(p0, p1);
       psum[e & 1] = add_pair<T>(pk[t4][e], psum[e & 1]);
     }
+  }
   return psum[0] + psum[1];
 }
 
@@ -91,12 +98,17 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
   const int half = lane >> 5, l32 = lane & 31;
   const int qrow = 32 * w + l32;
 
+  // On the diagonal block, wave w's query rows 32w .. 32w+31 see keys of the
+  // 32-key tiles 0 .. w only: the S and P.V MFMAs of later tiles are skipped
+  // (their P is 0), tiles before w need no mask and tile w the per-element one.
+  const int live = DIAG ? w + 1 : KT;
   // entered with K of this block landed in every wave's part and the barrier
   // passed (V may still be in flight)
   f32x16 s[KT];
 #pragma unroll
   for (int t4 = 0; t4 < KT; ++t4) {
     s[t4] = f32x16{};
+    if (DIAG && t4 >= live) continue;
     const int r = 32 * t4 + l32;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -110,12 +122,14 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
 
   if constexpr (DIAG) {  // key > query is masked on the diagonal block
 #pragma unroll
-    for (int t4 = 0; t4 < KT; ++t4)
+    for (int t4 = 0; t4 < KT; ++t4) {
+      if (t4 < w) continue;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int key = 32 * t4 + 8 * (v >> 2) + 4 * half + (v & 3);
-        if (key > qrow) s[t4][v] = -INFINITY;
+        if (t4 > w || key > qrow) s[t4][v] = -INFINITY;
       }
+    }
   }
   // P rounded to the input type, packed as the B operands of P.V, is first
   // formed against the running max; l adds the rounded P that P.V consumes.
@@ -128,7 +142,7 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
   float ps = 0.0f;
   bool move = first;
   if (!first) {
-    ps = exp_pack<T, KT>(s, st.m_run, c, pk);
+    ps = exp_pack<T, KT>(s, st.m_run, c, live, pk);
     move = __ballot(!(ps <= kRescaleSum)) != 0;
   }
   if (move) {
@@ -146,7 +160,7 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int v = 0; v < 16; ++v) st.o[dt][v] *= alpha;
-    ps = exp_pack<T, KT>(s, st.m_run, c, pk);
+    ps = exp_pack<T, KT>(s, st.m_run, c, live, pk);
   }
   st.l_part += ps;
 
@@ -164,6 +178,7 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
 #pragma unroll
   for (int u = 0; u < BLK / 16; ++u) {
     const int t4 = u >> 1, hh = u & 1;
+    if (DIAG && t4 >= live) continue;
     const uint4 pu = make_uint4(pk[t4][4 * hh], pk[t4][4 * hh + 1], pk[t4][4 * hh + 2],
                                 pk[t4][4 * hh + 3]);
     const typename T::vec8 pb = __builtin_bit_cast(typename T::vec8, pu);
