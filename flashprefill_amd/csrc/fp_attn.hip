@@ -205,12 +205,14 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
   }
 }
 
-// BLK = 128: 4 waves, 64 KB of LDS (d = 128), two workgroups per CU;
-// BLK = 64: 2 waves, 32 KB, four workgroups per CU. Either way two waves per
-// SIMD (the second launch bound is waves per execution unit), i.e. at most
-// 256 registers per wave.
-template <typename T, int D, int BLK>
-__global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
+// One work slot of the attention grid: a chunk unit (slot < unit_slots) or
+// a row. Every wave returns together (the early returns depend on the slot
+// only). The K and V buffers are the workgroup's static LDS. `tail()` runs
+// once the slot's last block is done, before the output is normalised and
+// stored (the persistent grid claims its next slot there, so the claim's
+// latency passes behind the stores); returns whether it ran.
+template <typename T, int D, int BLK, typename Args, typename Tail>
+__device__ __forceinline__ bool attn_slot(const Args& a, int slot, int t, Tail tail) {
   constexpr int CH = D / 8;   // 16-byte chunks per row
   constexpr int KS = D / 16;  // MFMA k-steps over the head dim
   constexpr int DT = D / 32;  // 32-row tiles of O^T
@@ -218,7 +220,7 @@ __global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
   __shared__ uint4 sk[BLK * CH];
   __shared__ uint4 sv[BLK * CH];
 
-  // Work item: the first unit_slots workgroups take the chunks of the split
+  // Work item: the first unit_slots slots take the chunks of the split
   // rows (a slice of a dense row's list, fp32 partials out), the others one
   // (head, sequence, q-block) row each through map_row. For a row, the item
   // record, the row record written by the selection stage (count, first two
@@ -229,11 +231,11 @@ __global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
   int h, ncnt, j0, jraw, unit = -1;
   bool has_diag;
   int64_t first = 0;  // list offset of the chunk
-  if (static_cast<int64_t>(blockIdx.x) < a.unit_slots) {
+  if (slot < a.unit_slots) {
     int u;
-    map_item(blockIdx.x, a.Hq, u, h);
+    map_item(static_cast<int>(slot), a.Hq, u, h);
     const int nunits = sld(a.units);
-    if (u >= nunits) return;
+    if (u >= nunits) return false;
     const UnitRec ur =
         sld(reinterpret_cast<const UnitRec*>(reinterpret_cast<const char*>(a.units) + 64) + u);
     rec = ur.r;
@@ -248,7 +250,7 @@ __global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
     unit = u;
   } else {
     int item;
-    map_row(static_cast<int>(blockIdx.x - a.unit_slots), a.Hq, a.Hkv, a.nb_sum_cap, item, h);
+    map_row(static_cast<int>(slot - a.unit_slots), a.Hq, a.Hkv, a.nb_sum_cap, item, h);
     const int64_t nitems = sld(a.tab.seq_tile + a.B);
     // map_row can return items up to 8 / Hkv - 1 past the table's capacity;
     // those (and any item >= nitems) return below, so the loads are clamped
@@ -256,9 +258,9 @@ __global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
     rec = sld(a.tab.items + it);
     const int4 rrec = sld(reinterpret_cast<const int4*>(a.rowrec) +
                           static_cast<int64_t>(h) * a.nb_sum_cap + it);
-    if (item >= nitems) return;
+    if (item >= nitems) return false;
     // the chunks of a split row produce its output
-    if (row_is_split(rec.i, (rec.L + BLK - 1) / BLK, a.last_n, a.split_blocks)) return;
+    if (row_is_split(rec.i, (rec.L + BLK - 1) / BLK, a.last_n, a.split_blocks)) return false;
     // counts and entries come from the search stage; clamp them to the row's
     // capacity so a stale workspace can never index outside the sequence
     ncnt = min(max(rrec.x, 0), rec.i + 1);
@@ -273,7 +275,7 @@ __global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
   const int32_t* list = a.idx + row_tri + first;
   const int kvh = h / (a.Hq / a.Hkv);
 
-  const int t = threadIdx.x, lane = t & 63;
+  const int lane = t & 63;  // t: threadIdx.x
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // wave index, kept in an SGPR
   const int half = lane >> 5, l32 = lane & 31;
   const int qrow = 32 * w + l32;           // query row inside the block
@@ -333,6 +335,7 @@ __global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
                            list, unused, L, c, nplain == 0, w, lane);
   }
 
+  tail();
   const float l = pair32_sum(st.l_part);
   if (unit >= 0) {
     // chunk of a split row: unnormalised O^T, the running max and l, for k_merge
@@ -350,7 +353,7 @@ __global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
       pp[BLK * D + qrow] = st.m_run;
       pp[BLK * D + BLK + qrow] = l;
     }
-    return;
+    return true;
   }
   const float rcp = 1.0f / l;
   if (qvalid) {
@@ -365,6 +368,69 @@ __global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
         pk.y = pack2<T>(st.o[dt][4 * g4 + 2] * rcp, st.o[dt][4 * g4 + 3] * rcp);
         *reinterpret_cast<uint2*>(op + d) = pk;
       }
+  }
+  return true;
+}
+
+// BLK = 128: 4 waves, 64 KB of LDS (d = 128), two workgroups per CU;
+// BLK = 64: 2 waves, 32 KB, four workgroups per CU. Either way two waves per
+// SIMD (the second launch bound is waves per execution unit), i.e. at most
+// 256 registers per wave.
+//
+// PERSIST = false: one workgroup per slot (grid = total_slots), in slot order.
+// PERSIST = true: a resident grid (a multiple of 8 workgroups, as many as fit)
+// whose workgroups on XCD x = id % 8 take the slots x, x + 8, x + 16, ...:
+// each its own id first, then claims from queue[x] one at a time, i.e. the
+// slots of an XCD in the same order the hardware dispatcher would give them,
+// without its gaps between a finished row and the next workgroup. A slot past
+// total_slots ends the workgroup's loop; the last claim of a queue empties it
+// for the next launch.
+template <typename T, int D, int BLK, bool PERSIST>
+__global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
+  // The arguments are read from the kernel-argument segment through a
+  // pointer (made opaque on every pass of the persistent loop, so that the
+  // compiler reloads them per slot with scalar loads instead of keeping ~70 of
+  // them live in SGPRs across the loop, which spills).
+  const __attribute__((address_space(4))) AttnArgs* ap =
+      (const __attribute__((address_space(4))) AttnArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+  if constexpr (!PERSIST) {
+    attn_slot<T, D, BLK>(*ap, static_cast<int>(blockIdx.x), static_cast<int>(threadIdx.x), [] {});
+  } else {
+    __shared__ int claim;
+    const int x = static_cast<int>(blockIdx.x & 7);
+    // the first slot of workgroup b is slot b itself (no claim); the queue of
+    // XCD x then hands out its later slots 8 (G + k) + x, k = 0, 1, ..., where
+    // G = gridDim.x / 8 workgroups run on each XCD
+    const int64_t g8 = gridDim.x >> 3;
+    // Claim of the next slot by thread 0 into `claim`. Re-arm: every
+    // workgroup of XCD x whose first slot was valid claims until one claim
+    // fails, so the claims of this launch end at k = valid + claimers - 1;
+    // the workgroup that gets it has made the queue's last access and
+    // empties it for the next launch.
+    auto claim_next = [&] {
+      if (threadIdx.x == 0) {
+        const int k = atomicAdd(&ap->queue[x], 1);
+        claim = k;
+        const int64_t per_x = (ap->total_slots - x + 7) >> 3;  // slots of XCD x
+        const int64_t valid = per_x > g8 ? per_x - g8 : 0;      // claimable ones
+        const int64_t claimers = per_x < g8 ? per_x : g8;
+        if (k == valid + claimers - 1) atomicExch(&ap->queue[x], 0);
+      }
+    };
+    int64_t slot = blockIdx.x;
+    for (;;) {
+      asm volatile("" : "+s"(ap));
+      if (slot >= ap->total_slots) break;
+      // the thread index is made opaque per slot, so that lane-derived values
+      // (tile-load offsets, operand addresses) are formed per slot rather than
+      // hoisted out of this loop, where they would stay live across it
+      int t = static_cast<int>(threadIdx.x);
+      asm volatile("" : "+v"(t));
+      if (!attn_slot<T, D, BLK>(*ap, static_cast<int>(slot), t, claim_next)) claim_next();
+      __syncthreads();  // K / V buffers are free and `claim` is set
+      slot = 8 * (g8 + claim) + x;
+      __syncthreads();  // every wave has read `claim`
+    }
   }
 }
 
@@ -438,10 +504,15 @@ __global__ __launch_bounds__(256) void k_merge(AttnArgs a) {
 }
 
 template <typename T, int D>
-hipError_t launch_attn_t(const AttnArgs& a, int block, int64_t grid, hipStream_t s) {
+hipError_t launch_attn_t(const AttnArgs& a, int block, int64_t grid, bool persist, hipStream_t s) {
   const dim3 g(static_cast<unsigned>(grid));
-  if (block == 128) hipLaunchKernelGGL((k_attn<T, D, 128>), g, dim3(256), 0, s, a);
-  else hipLaunchKernelGGL((k_attn<T, D, 64>), g, dim3(128), 0, s, a);
+  if (block == 128) {
+    if (persist) hipLaunchKernelGGL((k_attn<T, D, 128, true>), g, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((k_attn<T, D, 128, false>), g, dim3(256), 0, s, a);
+  } else {
+    if (persist) hipLaunchKernelGGL((k_attn<T, D, 64, true>), g, dim3(128), 0, s, a);
+    else hipLaunchKernelGGL((k_attn<T, D, 64, false>), g, dim3(128), 0, s, a);
+  }
   return hipGetLastError();
 }
 
@@ -466,13 +537,13 @@ hipError_t launch_merge(const AttnArgs& a, int dtype, int head_dim, int block, h
 }
 
 hipError_t launch_attn(const AttnArgs& a, int dtype, int head_dim, int block, int64_t grid,
-                       hipStream_t s) {
+                       bool persist, hipStream_t s) {
   if (grid <= 0) return hipSuccess;
   if (dtype == FP_DTYPE_BF16)
-    return head_dim == 128 ? launch_attn_t<BF16, 128>(a, block, grid, s)
-                           : launch_attn_t<BF16, 64>(a, block, grid, s);
-  return head_dim == 128 ? launch_attn_t<F16, 128>(a, block, grid, s)
-                         : launch_attn_t<F16, 64>(a, block, grid, s);
+    return head_dim == 128 ? launch_attn_t<BF16, 128>(a, block, grid, persist, s)
+                           : launch_attn_t<BF16, 64>(a, block, grid, persist, s);
+  return head_dim == 128 ? launch_attn_t<F16, 128>(a, block, grid, persist, s)
+                         : launch_attn_t<F16, 64>(a, block, grid, persist, s);
 }
 
 }  // namespace fp

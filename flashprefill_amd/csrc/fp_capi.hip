@@ -153,6 +153,31 @@ fp::SeqTables tables(const fp_ws_layout& L, void* ws) {
   return t;
 }
 
+// Workgroups of the attention kernel resident on the current device at once:
+// two per CU at block 128 (64 KB of LDS, 4 waves), four at block 64 (32 KB,
+// 2 waves), rounded up to a multiple of the 8 XCDs. The CU count is read once
+// per device.
+int resident_attn_workgroups(int block, int64_t* out) {
+  constexpr int kDevs = 64;
+  static std::mutex mu;
+  static int cus[kDevs] = {};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kDevs) return fail(FP_E_UNSUPPORTED, "device index %d", dev);
+  std::lock_guard<std::mutex> lock(mu);
+  if (cus[dev] == 0) {
+    int n = 0;
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(CU count)");
+    if (n < 1) return fail(FP_E_LAUNCH, "device reports %d CUs", n);
+    cus[dev] = n;
+  }
+  const int64_t per_cu = block == 128 ? 2 : 4;
+  *out = (cus[dev] * per_cu + 7) / 8 * 8;
+  return FP_OK;
+}
+
 float sm_scale_log2(int head_dim) {
   // fp32(1/sqrt(d)) * fp32(log2 e) in fp32, as the reference kernels compute it
   const float scale = static_cast<float>(1.0 / sqrt(static_cast<double>(head_dim)));
@@ -276,11 +301,25 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   a.part = reinterpret_cast<float*>(base + L.part_off);
   a.unit_cap = L.unit_cap;
   a.unit_slots = (static_cast<int64_t>(p->num_q_heads) * L.unit_cap + 7) / 8 * 8;
-  const int64_t grid =
-      a.unit_slots + fp::attn_grid(p->num_q_heads, p->num_kv_heads, L.nb_sum_cap);
-  hipError_t e = p->dtype == FP_DTYPE_F32
-                     ? fp::launch_attn_f32(a, p->head_dim, p->block_size, grid, s)
-                     : fp::launch_attn(a, p->dtype, p->head_dim, p->block_size, grid, s);
+  a.total_slots = a.unit_slots + fp::attn_grid(p->num_q_heads, p->num_kv_heads, L.nb_sum_cap);
+  a.queue = reinterpret_cast<int32_t*>(base + L.units_off) + fp::kQueueOff;
+  hipError_t e;
+  if (p->dtype == FP_DTYPE_F32) {
+    e = fp::launch_attn_f32(a, p->head_dim, p->block_size, a.total_slots, s);
+  } else {
+    // Persistent grid (every resident workgroup loops over its XCD's queue)
+    // once there are at least 8 slots per resident workgroup: it saves the
+    // dispatcher's gap between a finished row and the next workgroup
+    // (128K attention -3 to -4.5 %, 16K -1.7 %). Below that, one workgroup
+    // per slot (the persistent loop's per-slot claim costs more than it saves
+    // on short rows: 4K +6 %, 8K +4 %).
+    int64_t resident = 0;
+    const int rc = resident_attn_workgroups(p->block_size, &resident);
+    if (rc != FP_OK) return rc;
+    const bool persist = a.total_slots >= 8 * resident;
+    const int64_t grid = persist ? resident : a.total_slots;
+    e = fp::launch_attn(a, p->dtype, p->head_dim, p->block_size, grid, persist, s);
+  }
   if (e == hipSuccess && L.split_blocks > 0)
     e = fp::launch_merge(a, p->dtype, p->head_dim, p->block_size, s);
   return e == hipSuccess ? FP_OK : hip_fail(e, "attention launch");

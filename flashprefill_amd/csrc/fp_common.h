@@ -177,6 +177,14 @@ struct UnitRec {
   int32_t pad[2];
 };
 
+// Work queues of the persistent attention grid, in the header of the units
+// region (int32 words kQueueOff ..): one claim counter per XCD. The plan
+// kernel zeroes them on every call and the attention kernel empties each
+// queue again after its last claim, so that an attention launch on its own
+// (after one full call) also starts from empty queues.
+constexpr int kQueueOff = 4;
+constexpr int kQueueWords = 8;
+
 // The rule shared by the plan (which emits the chunks) and the attention
 // kernel (which leaves such rows to the chunks): row i of a sequence of nb
 // blocks is split when it is one of the last_n rows and has more than

@@ -19,7 +19,7 @@ struct PlanArgs {
   int32_t block;       // tokens per block
   int32_t last_n;      // last_n_block of the selection
   int32_t split_blocks;  // blocks per chunk of a split row (0: none)
-  int32_t* units;      // chunk units: count at [0], records from byte 64
+  int32_t* units;      // chunk units: count at [0], queue words, records from byte 64
   int64_t unit_cap;
 };
 
@@ -77,6 +77,10 @@ struct AttnArgs {
   float* part;
   int64_t unit_cap;
   int64_t unit_slots;
+  // persistent grid: the workgroups of XCD x (id % 8) claim the slots
+  // x, x + 8, x + 16, ... < total_slots from queue[x] (queue = units + kQueueOff)
+  int32_t* queue;
+  int64_t total_slots;
 };
 
 struct KvCacheArgs {
@@ -119,7 +123,7 @@ hipError_t launch_pool(const PoolArgs& a, int dtype, int head_dim, int64_t grid,
 hipError_t launch_search(const SearchArgs& a, int dtype, int head_dim, int block, int64_t grid,
                          bool from_scores, hipStream_t s);
 hipError_t launch_attn(const AttnArgs& a, int dtype, int head_dim, int block, int64_t grid,
-                       hipStream_t s);
+                       bool persist, hipStream_t s);
 // combines the chunk partials of the split rows into their output rows
 hipError_t launch_merge(const AttnArgs& a, int dtype, int head_dim, int block, hipStream_t s);
 hipError_t launch_attn_f32(const AttnArgs& a, int head_dim, int block, int64_t grid,

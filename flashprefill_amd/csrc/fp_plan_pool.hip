@@ -184,6 +184,7 @@ __global__ __launch_bounds__(1024) void k_plan(PlanArgs a) {
     s_pre[a.B] = static_cast<int32_t>(carry_tile);
     a.units[0] = static_cast<int32_t>(min(carry_unit, a.unit_cap));
   }
+  if (t < kQueueWords) a.units[kQueueOff + t] = 0;  // empty attention work queues
   __syncthreads();
 
   // 3. level sizes c_i = #{b : NB_b > i} (suffix sum of the histogram), then

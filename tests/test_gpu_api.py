@@ -151,6 +151,54 @@ def test_growing_logits_rescale(step):
     _close(o, ref.permute(1, 0, 2).cpu())
 
 
+@pytest.mark.parametrize("block", [128, 64])
+def test_persistent_attention_queues_rearm(block):
+    # 16K tokens x 32 heads gives at least 8 attention slots per resident
+    # workgroup at either block size, so the attention stage runs as the
+    # persistent grid over per-XCD claim queues. The plan kernel empties the
+    # queues once; every attention launch after that must empty them again
+    # itself: attention-only launches repeated on the planned workspace, and
+    # a second full call, give the first call's output bit for bit.
+    T, Hq, Hkv, d = 16384 if block == 128 else 32768, 32, 8, 128
+    q, k, v = (_rand((T, Hq, d), 41, scale=1.5).to(DEV), _rand((T, Hkv, d), 42, scale=1.5).to(DEV),
+               _rand((T, Hkv, d), 43).to(DEV))
+    cu = torch.tensor([0, T], dtype=torch.int32, device=DEV)
+    o = torch.empty_like(q)
+    call = FlashPrefillCall(q, k, v, o, cu, T, alpha=0.18, block_size=block)
+    call.run()
+    torch.cuda.synchronize()
+    ref = o.clone()
+    for _ in range(3):
+        o.fill_(float("nan"))
+        call.attn()
+        torch.cuda.synchronize()
+        assert torch.equal(o, ref)
+    o.fill_(float("nan"))
+    call.run()
+    torch.cuda.synchronize()
+    assert torch.equal(o, ref)
+    # sampled rows against the oracle's row pipeline (rows whose selection
+    # differs by a threshold flip are skipped; at most one is allowed)
+    tile, tri, _, _ = call.seq_tables()
+    nb = tile[-1]
+    cnt, idx = call.counts().cpu(), call.index_lists().cpu()
+    rows = [(h, i) for h in (0, 13, 31) for i in (0, nb // 3, nb - 1)]
+    res = O.flashprefill_rows(q.cpu(), k.cpu(), v.cpu(), rows, alpha=0.18, attention_sink=2,
+                              window=4, last_n=2, native=False, block=block)
+    flips = 0
+    for (h, i), (sel_o, out_o) in res.items():
+        base = tri[0] + i * (i + 1) // 2
+        gsel = torch.zeros(nb, dtype=torch.bool)
+        gsel[idx[h, base:base + int(cnt[h, i])].long()] = True
+        if not torch.equal(gsel, sel_o):
+            flips += int((gsel != sel_o).sum())
+            continue
+        got = o[i * block:(i + 1) * block, h].float().cpu()
+        d_ = (got - out_o.float()).abs()
+        assert d_.max().item() <= OUT_MAX_ABS and d_.mean().item() <= OUT_MEAN_ABS
+    assert flips <= 1
+
+
 def test_status_flags_and_untouched_output():
     T, Hq, Hkv, d = 1000, 4, 1, 128
     q, k, v = _rand((T, Hq, d), 11).to(DEV), _rand((T, Hkv, d), 12).to(DEV), _rand((T, Hkv, d), 13).to(DEV)
