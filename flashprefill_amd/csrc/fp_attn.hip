@@ -105,15 +105,29 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
   // entered with K of this block landed in every wave's part and the barrier
   // passed (V may still be in flight)
   f32x16 s[KT];
+  if constexpr (!DIAG) {
+    // k-step outer, tile inner: four independent accumulation chains
 #pragma unroll
-  for (int t4 = 0; t4 < KT; ++t4) {
-    s[t4] = f32x16{};
-    if (DIAG && t4 >= live) continue;
-    const int r = 32 * t4 + l32;
+    for (int t4 = 0; t4 < KT; ++t4) s[t4] = f32x16{};
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const uint4 kop = sk[r * CH + ((2 * ks + half) ^ swz<D>(r))];
-      s[t4] = T::mfma32(as_vec8<T>(kop), qb[ks], s[t4]);
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int t4 = 0; t4 < KT; ++t4) {
+        const int r = 32 * t4 + l32;
+        const uint4 kop = sk[r * CH + ((2 * ks + half) ^ swz<D>(r))];
+        s[t4] = T::mfma32(as_vec8<T>(kop), qb[ks], s[t4]);
+      }
+  } else {
+#pragma unroll
+    for (int t4 = 0; t4 < KT; ++t4) {
+      s[t4] = f32x16{};
+      if (t4 >= live) continue;
+      const int r = 32 * t4 + l32;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const uint4 kop = sk[r * CH + ((2 * ks + half) ^ swz<D>(r))];
+        s[t4] = T::mfma32(as_vec8<T>(kop), qb[ks], s[t4]);
+      }
     }
   }
   lds_barrier();  // every wave is done with the K buffer

@@ -151,17 +151,19 @@ def test_growing_logits_rescale(step):
     _close(o, ref.permute(1, 0, 2).cpu())
 
 
-@pytest.mark.parametrize("block", [128, 64])
-def test_persistent_attention_queues_rearm(block):
-    # 16K tokens x 32 heads gives at least 8 attention slots per resident
-    # workgroup at either block size, so the attention stage runs as the
-    # persistent grid over per-XCD claim queues. The plan kernel empties the
-    # queues once; every attention launch after that must empty them again
-    # itself: attention-only launches repeated on the planned workspace, and
-    # a second full call, give the first call's output bit for bit.
-    T, Hq, Hkv, d = 16384 if block == 128 else 32768, 32, 8, 128
-    q, k, v = (_rand((T, Hq, d), 41, scale=1.5).to(DEV), _rand((T, Hkv, d), 42, scale=1.5).to(DEV),
-               _rand((T, Hkv, d), 43).to(DEV))
+@pytest.mark.parametrize("block,dtype,d", [(128, torch.bfloat16, 128), (64, torch.bfloat16, 128),
+                                           (128, torch.float16, 64)])
+def test_persistent_attention_queues_rearm(block, dtype, d):
+    # 16K (block 128) / 32K (block 64) tokens x 32 heads give at least 8
+    # attention slots per resident workgroup, so the attention stage runs as
+    # the persistent grid over per-XCD claim queues. The plan kernel empties
+    # the queues once; every attention launch after that must empty them
+    # again itself: attention-only launches repeated on the planned
+    # workspace, and a second full call, give the first call's output bit for
+    # bit.
+    T, Hq, Hkv = 16384 if block == 128 else 32768, 32, 8
+    q, k, v = (_rand((T, Hq, d), 41, dtype, scale=1.5).to(DEV),
+               _rand((T, Hkv, d), 42, dtype, scale=1.5).to(DEV), _rand((T, Hkv, d), 43, dtype).to(DEV))
     cu = torch.tensor([0, T], dtype=torch.int32, device=DEV)
     o = torch.empty_like(q)
     call = FlashPrefillCall(q, k, v, o, cu, T, alpha=0.18, block_size=block)
