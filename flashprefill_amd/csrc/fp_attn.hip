@@ -72,6 +72,15 @@ __device__ __forceinline__ float exp_pack(const f32x16 (&s)[KT], float m, float 
   return psum[0] + psum[1];
 }
 
+// Instruction classes of __builtin_amdgcn_sched_group_barrier and how many
+// MFMAs ahead of its use each LDS operand read is issued in the S and P.V
+// loops. Left to itself the scheduler issued the reads one or two MFMAs ahead
+// (a wait before nearly every MFMA); four ahead measured 8 % faster at 128K
+// (two: 6 %, six or eight: no better), with the same registers and no spills.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
+constexpr int kReadAhead = 4;
+
 // One selected block (`first`: the row's first, wave-uniform): S = K.Q^T,
 // online softmax, O += V^T.P^T, and the pipelined refills of the K / V
 // buffers with block `jn` (when jn >= 0). The list entry at `pf` (the block
@@ -117,6 +126,14 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
         const uint4 kop = sk[r * CH + ((2 * ks + half) ^ swz<D>(r))];
         s[t4] = T::mfma32(as_vec8<T>(kop), qb[ks], s[t4]);
       }
+    // the K operand reads run kReadAhead MFMAs ahead of their use
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kReadAhead, 0);
+#pragma unroll
+    for (int k = 0; k < KS * KT - kReadAhead; ++k) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, kReadAhead, 0);
   } else {
 #pragma unroll
     for (int t4 = 0; t4 < KT; ++t4) {
@@ -208,6 +225,15 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
       const uint4 va = make_uint4(lo2.x, lo2.y, hi2.x, hi2.y);
       st.o[dt] = T::mfma32(as_vec8<T>(va), pb, st.o[dt]);
     }
+  }
+  if constexpr (!DIAG) {  // the V^T reads (two per MFMA) run kReadAhead MFMAs ahead
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kReadAhead, 0);
+#pragma unroll
+    for (int k = 0; k < (BLK / 16) * DT - kReadAhead; ++k) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, kReadAhead, 0);
   }
   __builtin_amdgcn_s_setprio(0);
   if (jn >= 0) {
