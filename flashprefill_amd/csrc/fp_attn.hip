@@ -2,8 +2,10 @@
 // (ops/flashprefill_native_forward.py:227-344,
 //  ops/flashprefill_varlen_func.py:449-575).
 //
-// One workgroup (4 waves) owns one (query head h, sequence b, q-block i) item
-// and walks that row's selected key blocks in ascending order. Wave w owns the
+// A workgroup (4 waves) processes one (query head h, sequence b, q-block i)
+// item at a time and walks that row's selected key blocks in ascending order;
+// large problems run as a persistent grid whose workgroups claim the next item
+// of their XCD from a queue (k_attn below). Wave w owns the
 // 32 query rows 32w..32w+31 of the block. Everything is kept in the
 // "one query per lane" orientation so the softmax never needs a cross-lane
 // transpose:
