@@ -9,13 +9,16 @@ from 12 on also vary the block size (64 / 128) and include fp32 inputs. The sequ
 so sink / window / last-n rules keep most blocks: these cases stress the
 edges (1-token and partial blocks, GQA ratios, d = 64, fp16, native mode,
 min_budget); sparse selection at length is covered by the structured 4K and
-128K tests."""
+128K tests. Four larger seeded cases (ragged batches of 19K-55K tokens from
+the structured synthetic distribution, sampled attention rows) are sized so
+that the attention stage runs as the persistent grid."""
 
 import random
 
 import pytest
 import torch
 
+from flashprefill_amd import synth
 from tests._parity import (OUT_MAX_ABS, OUT_MAX_ABS_F32, OUT_MEAN_ABS, OUT_MEAN_ABS_F32,
                            run_stages)
 
@@ -87,3 +90,58 @@ def test_random_configuration(seed):
     f32 = dtype == torch.float32
     assert rep.out_max_abs <= (OUT_MAX_ABS_F32 if f32 else OUT_MAX_ABS)
     assert rep.out_mean_abs <= (OUT_MEAN_ABS_F32 if f32 else OUT_MEAN_ABS)
+
+
+def _large_case(seed):
+    """Ragged batches large enough that the attention stage runs as the
+    persistent grid (at least 8 work slots per resident workgroup)."""
+    rnd = random.Random(seed)
+    block = rnd.choice([64, 128])
+    hkv = rnd.choice([2, 4, 8])
+    hq = hkv * rnd.choice([4, 7, 8]) if hkv < 8 else 32
+    d = rnd.choice([64, 128])
+    dtype = rnd.choice([torch.bfloat16, torch.float16])
+    nseq = rnd.randint(2, 4)
+    lens = [rnd.choice([rnd.randint(1, 300), rnd.randint(2000, 9000), rnd.randint(9000, 24000)])
+            for _ in range(nseq)]
+    params = dict(alpha=rnd.choice([0.05, 0.12, 0.18]), sink=rnd.randint(0, 3),
+                  window=rnd.randint(1, 6), last_n=rnd.randint(0, 3))
+    return lens, hq, hkv, d, dtype, params, block
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_random_large_configuration_persistent_attention(seed):
+    lens, hq, hkv, d, dtype, params, block = _large_case(2000 + seed)
+    per_cu = 2 if block == 128 else 4
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    # grow the longest sequence until Hq * (capacity of the block table) reaches
+    # 8 slots per resident workgroup, the host's threshold for the persistent grid
+    while True:
+        nb_max = (max(lens) + block - 1) // block
+        cap = min(len(lens) * nb_max, (sum(lens) + (block - 1) * len(lens)) // block)
+        if hq * cap >= 8 * per_cu * cus:
+            break
+        lens[lens.index(max(lens))] += 4096
+    # the structured synthetic distribution of the benchmark (sinks, stripes,
+    # a rotary local band, hot blocks): sparse selections with ragged lists
+    spec = synth.SynthSpec(seq_lens=tuple(lens), num_q_heads=hq, num_kv_heads=hkv, head_dim=d,
+                           dtype=dtype, seed=seed, block=block)
+    q, k, v, cu_t = synth.make_inputs(spec, device="cpu")
+    cu = [int(x) for x in cu_t]
+    rows = {}
+    for b, n in enumerate(lens):
+        nb = (n + block - 1) // block
+        rows[b] = sorted({(h, i) for h in (0, hq // 2, hq - 1) for i in (0, nb // 2, nb - 1)})
+    print(f"\n  seed={seed} lens={lens} hq={hq} hkv={hkv} d={d} {dtype} block={block} {params}",
+          flush=True)
+    rep = run_stages(q, k, v, cu, max(lens), block=block, attn_rows=rows, **params)
+    print(f"  flips={rep.e2e_flips}/{rep.cells} density={rep.density:.3f} "
+          f"out_max={rep.out_max_abs:.2e} out_mean={rep.out_mean_abs:.2e}", flush=True)
+    assert rep.pool_ulp <= 1
+    assert rep.m_max_rel < 1e-4
+    assert rep.p_max_rel < 1e-3
+    assert rep.sel_from_gpu_scores_mismatch == 0
+    assert rep.sel_from_oracle_scores_mismatch == 0
+    assert rep.e2e_flips <= max(2, 2e-3 * rep.cells)
+    assert rep.out_max_abs <= OUT_MAX_ABS
+    assert rep.out_mean_abs <= OUT_MEAN_ABS
