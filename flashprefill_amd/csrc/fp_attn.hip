@@ -74,13 +74,10 @@ __device__ __forceinline__ float exp_pack(const f32x16 (&s)[KT], float m, float 
   return psum[0] + psum[1];
 }
 
-// Instruction classes of __builtin_amdgcn_sched_group_barrier and how many
-// MFMAs ahead of its use each LDS operand read is issued in the S and P.V
-// loops. Left to itself the scheduler issued the reads one or two MFMAs ahead
+// How many MFMAs ahead of its use each LDS operand read is issued in the S
+// and P.V loops (sched_group_barrier order). Left to itself the scheduler issued the reads one or two MFMAs ahead
 // (a wait before nearly every MFMA); four ahead measured 8 % faster at 128K
 // (two: 6 %, six or eight: no better), with the same registers and no spills.
-constexpr int kSchedMfma = 0x008;
-constexpr int kSchedDsRead = 0x100;
 constexpr int kReadAhead = 4;
 
 // One selected block (`first`: the row's first, wave-uniform): S = K.Q^T,

@@ -14,6 +14,22 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
+// instruction classes of __builtin_amdgcn_sched_group_barrier
+constexpr int kSchedValu = 0x002;
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedVmemRead = 0x020;
+constexpr int kSchedDsRead = 0x100;
+
+// compile-time arguments of generic lambdas (unrolled pipeline stages)
+template <bool B>
+struct BoolC {
+  static constexpr bool value = B;
+};
+template <int N>
+struct IntC {
+  static constexpr int value = N;
+};
+
 // Load through the scalar cache: the address must be wave-uniform and the
 // data must not be written while the kernel runs (tables and index lists
 // written by earlier kernels of the stream).

@@ -101,10 +101,12 @@ int layout(const fp_problem* p, fp_ws_layout* L) {
   if (Hq * cap > (int64_t(1) << 31)) return fail(FP_E_INVALID_ARG, "too many work items");
   if (Hq * tri >= (int64_t(1) << 31))
     return fail(FP_E_UNSUPPORTED, "index lists of 2^31 entries or more are not supported");
-  // the search addresses a sequence's pooled keys with 32-bit byte offsets
+  // the search forms a lane's pooled-key offset (one chunk row of nb_sum_cap
+  // 16-byte entries, plus a key) in 32 bits; the batch and length bounds of
+  // validate() keep nb_sum_cap <= 4096 * 8192 = 2^25, this guards the rule
   const int64_t eb = elem_bytes(p->dtype);
-  if (nb_max * Hkv * d * eb >= (int64_t(1) << 31))
-    return fail(FP_E_UNSUPPORTED, "pooled keys of 2^31 bytes or more per sequence are not supported");
+  if (cap >= (int64_t(1) << 26))
+    return fail(FP_E_UNSUPPORTED, "2^26 or more key blocks in one call are not supported");
   size_t off = 0;
   L->status_off = off;     off = align_up(off + 4);
   L->seq_tile_off = off;   off = align_up(off + 8 * (B + 1));
@@ -220,6 +222,7 @@ int run_pool(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   a.kst = p->k_stride_tok;
   a.khs = p->k_stride_head;
   a.mk = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + L.mk_off);
+  a.nb_sum_cap = L.nb_sum_cap;
   a.B = p->batch;
   a.Hkv = p->num_kv_heads;
   a.block = p->block_size;

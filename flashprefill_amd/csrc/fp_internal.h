@@ -27,7 +27,8 @@ struct PoolArgs {
   SeqTables tab;
   const uint16_t* k;
   int64_t kst, khs;
-  uint16_t* mk;  // (sum NB, Hkv, D)
+  uint16_t* mk;  // chunk-major pooled keys (see fp_ws_layout in flashprefill.h)
+  int64_t nb_sum_cap;
   int32_t B;
   int32_t Hkv;
   int32_t block;  // tokens per block

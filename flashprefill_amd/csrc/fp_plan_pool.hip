@@ -230,7 +230,10 @@ __global__ __launch_bounds__(1024) void k_plan(PlanArgs a) {
 // D / 8 chunks of 16 bytes; each thread sums its rows of one chunk in fp32,
 // the R partial sums are added through LDS in row-group order and the mean is
 // rounded once. Several workgroups per block keep short sequences from
-// running on a handful of CUs.
+// running on a handful of CUs. The means are stored chunk-major (16-byte
+// chunk c of key block g and kv head hh at entry g of chunk row hh * C + c),
+// so that the search kernel's loads of 32 consecutive keys' chunk are
+// contiguous.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void k_pool(PoolArgs a) {
   constexpr int C = D / 8;    // 16-byte chunks per head row
@@ -268,7 +271,8 @@ __global__ __launch_bounds__(256) void k_pool(PoolArgs a) {
     uint16_t o[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) o[q] = T::from_f32(acc[q] * inv);
-    uint16_t* out = a.mk + (g * a.Hkv + hh) * static_cast<int64_t>(D) + c * 8;
+    // chunk-major: chunk c of (g, hh) is entry g of chunk row hh * C + c
+    uint16_t* out = a.mk + ((hh * C + c) * a.nb_sum_cap + g) * 8;
     st16(out, *reinterpret_cast<const uint4*>(o));
   }
 }
@@ -286,12 +290,14 @@ __global__ __launch_bounds__(256) void k_pool_f32(PoolArgs a, int head_dim) {
   const int64_t t0 = a.tab.seq_start[b] + static_cast<int64_t>(i) * a.block;
   const int rows = min(a.block, L - i * a.block);
   const float* k = reinterpret_cast<const float*>(a.k);
-  float* out = reinterpret_cast<float*>(a.mk) + (g * a.Hkv + hh) * static_cast<int64_t>(head_dim);
+  // chunk-major: dims 4c .. 4c+3 of (g, hh) are entry g of chunk row hh * d / 4 + c
+  float* out = reinterpret_cast<float*>(a.mk);
   for (int x = threadIdx.x; x < head_dim; x += blockDim.x) {
     const float* src = k + t0 * a.kst + hh * a.khs + x;
     double sum = 0.0;
     for (int r = 0; r < rows; ++r) sum += static_cast<double>(src[static_cast<int64_t>(r) * a.kst]);
-    out[x] = static_cast<float>(sum / static_cast<double>(rows));
+    const int64_t row = static_cast<int64_t>(hh) * (head_dim / 4) + x / 4;
+    out[(row * a.nb_sum_cap + g) * 4 + x % 4] = static_cast<float>(sum / static_cast<double>(rows));
   }
 }
 

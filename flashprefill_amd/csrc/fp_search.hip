@@ -245,25 +245,31 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
     const int half = lane >> 5, l32 = lane & 31;
     const float c = a.sm_scale_log2;
     constexpr int CH = D / 8;
-    const int64_t mk_row = static_cast<int64_t>(a.Hkv) * D;
-    // wave-uniform base of this kv head's pooled keys; the lane part of a
-    // load address is a 32-bit byte offset formed at each load
-    const char* mkb = reinterpret_cast<const char*>(a.mk + tile_b * mk_row +
-                                                    static_cast<int64_t>(kvh) * D);
-    // a sequence's pooled keys span < 2^31 bytes (checked on the host)
-    const int mk_row_b = static_cast<int>(mk_row) * 2;
+    // Pooled keys are chunk-major: 16-byte chunk x of key block g of kv head
+    // kvh at byte ((kvh * CH + x) * nb_sum_cap + g) * 16, so the chunk of 32
+    // consecutive keys that one k-step's operands need is 512 contiguous
+    // bytes. kbase[s]: wave-uniform base of chunk row 2 s (the lower
+    // half-wave's; the upper half-wave reads row 2 s + 1), at this sequence's
+    // first key; the lane part of an address is a 32-bit byte offset.
+    const char* kbase[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      kbase[s] = reinterpret_cast<const char*>(a.mk) +
+                 ((static_cast<int64_t>(kvh) * CH + 2 * s) * a.nb_sum_cap + tile_b) * 16;
+    // < 2^31: nb_sum_cap < 2^26 (checked on the host)
+    const uint32_t half_off = static_cast<uint32_t>(a.nb_sum_cap) * 16u * static_cast<uint32_t>(half);
     const int ntiles = (n + 31) >> 5;
-    // pooled keys of one 32-key tile as MFMA B operands (lane: key 32 tile + l32)
+    // pooled keys of one 32-key tile as MFMA B operands (lane: key 32 tile +
+    // l32, dims 16 s + 8 half .. +7; columns past the row's last key read key
+    // n - 1: their scores are computed and never stored)
     typename T::vec8 kb[KS];
     auto load_kb = [&](int tile) {
       int ln = lane;
       asm volatile("" : "+v"(ln));
-      const int j = 32 * tile + (ln & 31);
-      const bool jv = j < n;
-      const char* p = mkb + (j * mk_row_b + 16 * (ln >> 5));
+      const int j = min(32 * tile + (ln & 31), n - 1);
+      const uint32_t off = half_off + static_cast<uint32_t>(j) * 16u;
 #pragma unroll
-      for (int s = 0; s < KS; ++s)
-        kb[s] = as_vec8<T>(jv ? *reinterpret_cast<const uint4*>(p + 32 * s) : zero4());
+      for (int s = 0; s < KS; ++s) kb[s] = as_vec8<T>(*reinterpret_cast<const uint4*>(kbase[s] + off));
     };
     // stage the query block in LDS with direct-to-LDS loads (rows past the
     // sequence end are then zeroed: they still count for j < i); every wave
@@ -379,7 +385,10 @@ __global__ __launch_bounds__(256, 2) void k_search_f32(SearchArgs a) {
   const int kvh = h / (a.Hq / a.Hkv);
   const float c = a.sm_scale_log2;
   const float* q = reinterpret_cast<const float*>(a.q);
-  const float* mk = reinterpret_cast<const float*>(a.mk) + tile_b * a.Hkv * D + kvh * D;
+  // chunk-major pooled keys (4 floats per chunk): dims 4x .. 4x+3 of key block g
+  // at ((kvh * D / 4 + x) * nb_sum_cap + g) * 4
+  const float* mk = reinterpret_cast<const float*>(a.mk) +
+                    (static_cast<int64_t>(kvh) * (D / 4) * a.nb_sum_cap + tile_b) * 4;
 
   // query block -> LDS (rows past the sequence end are zero: they still
   // count for j < i)
@@ -396,10 +405,12 @@ __global__ __launch_bounds__(256, 2) void k_search_f32(SearchArgs a) {
     const int j = 32 * tile + l32;
     const bool jv = j < n;
     float kb[KS];
-    const float* kr = mk + static_cast<int64_t>(jv ? j : 0) * a.Hkv * D + half * KS;
+    // this lane's dims half * KS .. : chunks half * KS / 4 + s4
+    const float* kr = mk + (static_cast<int64_t>(half) * (KS / 4) * a.nb_sum_cap + (jv ? j : 0)) * 4;
 #pragma unroll
     for (int s4 = 0; s4 < KS / 4; ++s4) {
-      const float4 x = jv ? *reinterpret_cast<const float4*>(kr + 4 * s4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 x = jv ? *reinterpret_cast<const float4*>(kr + s4 * a.nb_sum_cap * 4)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
       kb[4 * s4] = x.x; kb[4 * s4 + 1] = x.y; kb[4 * s4 + 2] = x.z; kb[4 * s4 + 3] = x.w;
     }
     f32x16 acc[RG];

@@ -195,10 +195,14 @@ class FlashPrefillCall:
         return self._view(self.layout.items_off, torch.int32, 8 * tile[-1]).view(-1, 8)[:, :2]
 
     def pooled_k(self) -> torch.Tensor:
+        """Pooled K as (sum NB, Hkv, d); the workspace holds it chunk-major
+        (16-byte chunks of all key blocks of one (kv head, chunk) in a row)."""
         tile, _, _, _ = self.seq_tables()
-        n = tile[-1] * self.Hkv * self.d
-        return self._view(self.layout.mk_off, self.tensors[0].dtype, n).view(tile[-1], self.Hkv,
-                                                                              self.d)
+        cap, dt = self.layout.nb_sum_cap, self.tensors[0].dtype
+        e = 16 // torch.tensor([], dtype=dt).element_size()
+        raw = self._view(self.layout.mk_off, dt, self.Hkv * self.d * cap)
+        return (raw.view(self.Hkv, self.d // e, cap, e)[:, :, :tile[-1]]
+                .permute(2, 0, 1, 3).reshape(tile[-1], self.Hkv, self.d))
 
     def counts(self) -> torch.Tensor:
         L = self.layout

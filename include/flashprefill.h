@@ -93,7 +93,8 @@ typedef struct fp_problem {
 
 /* Where each intermediate lives inside the workspace (byte offsets), with the
  * index arithmetic the kernels use:
- *   pooled K   mk[(tile(b) + j) * Hkv * d + kvh * d + x]            (input dtype)
+ *   pooled K   mk[((kvh * d / e + x / e) * nb_sum_cap + tile(b) + j) * e + x % e]
+ *              (input dtype, e = 16 / element bytes: chunk-major 16-byte chunks)
  *   counts     cnt[h * nb_sum_cap + tile(b) + i]                    (int32)
  *   lists      idx[h * tri_cap + tri(b) + i*(i+1)/2 + n], n < cnt   (int32, ascending j)
  *   p/m dumps  same triangular index with j in place of n           (fp32)
