@@ -65,29 +65,47 @@ __device__ __forceinline__ uint4 ld16(const void* p) {
 __device__ __forceinline__ void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
 
 // ---------------------------------------------------------------------------
-// wave / block reductions (wave64)
+// wave reductions (wave64)
 // ---------------------------------------------------------------------------
+// Lane exchanges without an address register: v_permlane32_swap between the
+// two 32-lane halves, ds_swizzle (bit mode: and 0x1f, or 0, xor M) within a
+// half. The reductions are xor butterflies (distance 32, then 16 .. 1).
+// v_permlane32_swap(x, x): the first result holds x of lanes 0-31 in both
+// halves, the second x of lanes 32-63, so the partner of a lower lane is in
+// the second and that of an upper lane in the first.
+__device__ __forceinline__ uint32_t xchg32(uint32_t x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return (threadIdx.x & 32) ? static_cast<uint32_t>(r[0]) : static_cast<uint32_t>(r[1]);
+}
+template <int M>
+__device__ __forceinline__ uint32_t xchg_xor(uint32_t x) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_ds_swizzle(static_cast<int>(x), 0x1f | (M << 10)));
+}
 __device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
+  x = fmaxf(x, __uint_as_float(xchg32(__float_as_uint(x))));
+  x = fmaxf(x, __uint_as_float(xchg_xor<16>(__float_as_uint(x))));
+  x = fmaxf(x, __uint_as_float(xchg_xor<8>(__float_as_uint(x))));
+  x = fmaxf(x, __uint_as_float(xchg_xor<4>(__float_as_uint(x))));
+  x = fmaxf(x, __uint_as_float(xchg_xor<2>(__float_as_uint(x))));
+  return fmaxf(x, __uint_as_float(xchg_xor<1>(__float_as_uint(x))));
+}
+template <int M>
+__device__ __forceinline__ double xchg_xor_d(double x) {
+  const uint64_t u = __double_as_longlong(x);
+  const uint32_t lo = xchg_xor<M>(static_cast<uint32_t>(u));
+  const uint32_t hi = xchg_xor<M>(static_cast<uint32_t>(u >> 32));
+  return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
 }
 __device__ __forceinline__ double wave_sum_d(double x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
-  return x;
-}
-
-// Block-wide max over blockDim.x threads; `red` needs blockDim.x/64 floats.
-__device__ __forceinline__ float block_max(float x, float* red) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  x = wave_max(x);
-  if (lane == 0) red[w] = x;
-  __syncthreads();
-  float r = red[0];
-  for (int k = 1; k < nw; ++k) r = fmaxf(r, red[k]);
-  __syncthreads();
-  return r;
+  const uint64_t u = __double_as_longlong(x);
+  const uint32_t lo = xchg32(static_cast<uint32_t>(u)), hi = xchg32(static_cast<uint32_t>(u >> 32));
+  x += __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+  x += xchg_xor_d<16>(x);
+  x += xchg_xor_d<8>(x);
+  x += xchg_xor_d<4>(x);
+  x += xchg_xor_d<2>(x);
+  return x + xchg_xor_d<1>(x);
 }
 
 // Number of set bits of `mask` below this lane.

@@ -52,6 +52,7 @@ struct SearchArgs {
   float sm_scale_log2;  // fp32(fp32(1/sqrt(d)) * fp32(log2 e))
   float alpha;
   int32_t sink, window, last_n, native, min_budget;
+  int32_t pair_rows;  // 16-bit score kernel: two rows per workgroup (set by launch_search)
 };
 
 struct AttnArgs {

@@ -39,6 +39,19 @@ __device__ __forceinline__ uint32_t sort_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// The selection's workgroup barriers wait for LDS operations only
+// (lds_barrier): the waves exchange data through LDS alone, and a
+// direct-to-LDS load of the next row's query block may be in flight meanwhile.
+__device__ __forceinline__ float block_max_lds(float x, float* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  x = wave_max(x);
+  if (lane == 0) red[w] = x;
+  lds_barrier();
+  const float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  lds_barrier();
+  return r;
+}
+
 // LDS scratch of select_row: block-reduction slots and the radix histogram
 constexpr int kSelectScratch = 104 + 256 * 4;
 
@@ -48,19 +61,19 @@ constexpr int kSelectScratch = 104 + 256 * 4;
 // returns the key of the budget-th entry and, in `need_eq`, how many of the
 // entries with exactly that key are taken (lowest j first). Radix select over
 // the sortable 32-bit keys, 8 bits per pass, MSB first.
-__device__ uint32_t budget_threshold(const float* pl, int n, int kk, uint32_t* hist, int* pick,
+__device__ __forceinline__ uint32_t budget_threshold(const float* pl, int n, int kk, uint32_t* hist, int* pick,
                                      int& need_eq) {
   const int t = threadIdx.x, lane = t & 63;
   uint32_t prefix = 0, pmask = 0;
   int need = kk;
   for (int shift = 24; shift >= 0; shift -= 8) {
     hist[t] = 0;  // 256 bins, one per thread
-    __syncthreads();
+    lds_barrier();
     for (int j = t; j < n; j += 256) {
       const uint32_t key = sort_key(pl[j]);
       if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255], 1u);
     }
-    __syncthreads();
+    lds_barrier();
     if (t < 64) {  // wave 0: the bin holding the need-th largest key
       const int b0 = 255 - 4 * lane;  // this lane's bins b0 .. b0-3, descending
       const int c0 = hist[b0], c1 = hist[b0 - 1], c2 = hist[b0 - 2], c3 = hist[b0 - 3];
@@ -84,11 +97,11 @@ __device__ uint32_t budget_threshold(const float* pl, int n, int kk, uint32_t* h
         pick[1] = rem;
       }
     }
-    __syncthreads();
+    lds_barrier();
     prefix |= static_cast<uint32_t>(pick[0]) << shift;
     pmask |= 255u << shift;
     need = pick[1];
-    __syncthreads();  // pick and hist are rewritten by the next pass
+    lds_barrier();  // pick and hist are rewritten by the next pass
   }
   need_eq = need;
   return prefix;
@@ -97,15 +110,18 @@ __device__ uint32_t budget_threshold(const float* pl, int n, int kk, uint32_t* h
 // Select over p (pl) and m (ml) of one row held in LDS; writes the ascending
 // index list and its length. Uses 256 threads; `scratch` is kSelectScratch
 // bytes of LDS (the query block's area once scoring is done, so that the
-// kernel's LDS stays at 40 KB and four workgroups fit on a CU). ml is
-// overwritten (with the min_budget flags).
+// kernel's LDS stays at 40 KB and four workgroups fit on a CU), or, without
+// min_budget, the first 104 of them (the radix histogram is not used), which
+// the paired-row kernel takes from the unused tail of ml. ml is overwritten
+// (with the min_budget flags).
 //
 // Two block reductions: M = max_j m_j, then max_j S_j together with the
 // native row sum. Since the native division by (sum + 1e-9) is correctly
 // rounded and monotone, the max of the normalised scores is the normalised
 // max. The compaction loops use alternating count slots, one barrier per
 // 256 entries.
-__device__ void select_row(float* pl, float* ml, int n, int i, int nb, const SearchArgs& a,
+__device__ __forceinline__ void select_row(float* pl, float* ml, int n, int i, int nb,
+                                           const SearchArgs& a,
                            int32_t* list, int32_t* count, int32_t* row_rec, void* scratch) {
 #pragma clang fp contract(off)
   float* redf = static_cast<float*>(scratch);
@@ -119,7 +135,7 @@ __device__ void select_row(float* pl, float* ml, int n, int i, int nb, const Sea
 
   float lm = -INFINITY;
   for (int j = t; j < n; j += 256) lm = fmaxf(lm, ml[j]);
-  const float M = block_max(lm, redf);
+  const float M = block_max_lds(lm, redf);
 
   double ls = 0.0;
   float lmax = 0.0f;
@@ -135,7 +151,7 @@ __device__ void select_row(float* pl, float* ml, int n, int i, int nb, const Sea
     redf[w] = lmax;
     redd[w] = ls;
   }
-  __syncthreads();  // redf / redd are not written again in this row
+  lds_barrier();  // redf / redd are not written again in this row
   float maxS = fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
   if (a.native) {
     const float tot = static_cast<float>(redd[0] + redd[1] + redd[2] + redd[3]);
@@ -158,13 +174,13 @@ __device__ void select_row(float* pl, float* ml, int n, int i, int nb, const Sea
       const bool eq = j < n && key == kstar;
       const uint64_t bal = __ballot(eq);
       if (lane == 0) wtot[c2 + w] = __popcll(bal);
-      __syncthreads();
+      lds_barrier();
       int off = eq_running;
       for (int k = 0; k < w; ++k) off += wtot[c2 + k];
       if (j < n) ml[j] = (key > kstar || (eq && off + lanes_below(bal) < need_eq)) ? 1.0f : 0.0f;
       eq_running += wtot[c2] + wtot[c2 + 1] + wtot[c2 + 2] + wtot[c2 + 3];
     }
-    __syncthreads();  // the count slots are reused below
+    lds_barrier();  // the count slots are reused below
   }
 
   int running = 0;
@@ -178,7 +194,7 @@ __device__ void select_row(float* pl, float* ml, int n, int i, int nb, const Sea
     const uint64_t bal = __ballot(keep);
     // slot set c2 was last read before the previous chunk's barrier
     if (lane == 0) wtot[c2 + w] = __popcll(bal);
-    __syncthreads();
+    lds_barrier();
     int off = running;
     for (int k = 0; k < w; ++k) off += wtot[c2 + k];
     if (keep) {
@@ -189,7 +205,7 @@ __device__ void select_row(float* pl, float* ml, int n, int i, int nb, const Sea
     if (j == i) head3[2] = keep ? 1 : 0;
     running += wtot[c2] + wtot[c2 + 1] + wtot[c2 + 2] + wtot[c2 + 3];
   }
-  __syncthreads();  // head3 complete
+  lds_barrier();  // head3 complete
   if (t == 0) {
     *count = running;
     // the attention kernel's row record: one 16-byte load gives the count,
@@ -220,141 +236,203 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
   float* pl = reinterpret_cast<float*>(reinterpret_cast<char*>(dyn4) +
                                        search_q_bytes<D, BLK, FROM_SCORES>());
   float* ml = pl + a.nb_max;
-  int item, h;
-  map_item(blockIdx.x, a.Hq, item, h);
-  // the item record (one scalar load) carries everything the query-block
-  // loads need, so they are issued one scalar-load latency after the start
+  int slot, h;
+  map_item(blockIdx.x, a.Hq, slot, h);
   const int64_t nitems = sld(a.tab.seq_tile + a.B);
-  if (item >= nitems) return;
-  const ItemRec rec = sld(a.tab.items + item);
-  const int b = rec.b, i = rec.i, L = rec.L;
-  const int64_t tile_b = rec.tile - i;
-  const int64_t t0 = rec.t0;
-  const int n = i + 1;
-  const int64_t row_tri = static_cast<int64_t>(h) * a.tri_cap + rec.tri;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  // The workgroup's rows: item `slot`, and with pair_rows also the item at the
+  // other end of the heaviest-first order, so that every pair holds about the
+  // same work (scored second, its query block loads during the first row's
+  // selection).
+  const int64_t item_a = slot;
+  int64_t item_b = -1;
+  if (!FROM_SCORES && a.pair_rows) {
+    if (item_a >= (nitems + 1) / 2) return;
+    item_b = nitems - 1 - item_a;
+    if (item_b == item_a) item_b = -1;
+  } else if (item_a >= nitems) {
+    return;
+  }
+  auto select = [&](const ItemRec& rec, int64_t item, int64_t row_tri, void* scratch) {
+    int32_t* list = a.idx + row_tri;
+    int32_t* count = a.cnt + static_cast<int64_t>(h) * a.nb_sum_cap + rec.tile;
+    int32_t* row_rec = a.rowrec + 4 * (static_cast<int64_t>(h) * a.nb_sum_cap + item);
+    const int64_t tile_b = rec.tile - rec.i;
+    const int nb = static_cast<int>(sld(a.tab.seq_tile + rec.b + 1) - tile_b);
+    select_row(pl, ml, rec.i + 1, rec.i, nb, a, list, count, row_rec, scratch);
+  };
 
   if constexpr (FROM_SCORES) {
-    for (int j = t; j < n; j += 256) {
+    const ItemRec rec = sld(a.tab.items + item_a);
+    const int64_t row_tri = static_cast<int64_t>(h) * a.tri_cap + rec.tri;
+    for (int j = t; j <= rec.i; j += 256) {
       pl[j] = a.in_p[row_tri + j];
       ml[j] = a.in_m[row_tri + j];
     }
+    __syncthreads();
+    select(rec, item_a, row_tri, dyn4);
   } else {
     constexpr int KS = D / 16;  // MFMA k-steps over the head dim
+    constexpr int CH = D / 8;
     const int kvh = h / (a.Hq / a.Hkv);
     const int half = lane >> 5, l32 = lane & 31;
     const float c = a.sm_scale_log2;
-    constexpr int CH = D / 8;
+    // < 2^31: nb_sum_cap < 2^26 (checked on the host)
+    const uint32_t half_off = static_cast<uint32_t>(a.nb_sum_cap) * 16u * static_cast<uint32_t>(half);
+    // One row: its item record and the wave-uniform base of its pooled keys.
     // Pooled keys are chunk-major: 16-byte chunk x of key block g of kv head
     // kvh at byte ((kvh * CH + x) * nb_sum_cap + g) * 16, so the chunk of 32
     // consecutive keys that one k-step's operands need is 512 contiguous
-    // bytes. kbase[s]: wave-uniform base of chunk row 2 s (the lower
-    // half-wave's; the upper half-wave reads row 2 s + 1), at this sequence's
-    // first key; the lane part of an address is a 32-bit byte offset.
-    const char* kbase[KS];
-#pragma unroll
-    for (int s = 0; s < KS; ++s)
-      kbase[s] = reinterpret_cast<const char*>(a.mk) +
-                 ((static_cast<int64_t>(kvh) * CH + 2 * s) * a.nb_sum_cap + tile_b) * 16;
-    // < 2^31: nb_sum_cap < 2^26 (checked on the host)
-    const uint32_t half_off = static_cast<uint32_t>(a.nb_sum_cap) * 16u * static_cast<uint32_t>(half);
-    const int ntiles = (n + 31) >> 5;
+    // bytes. kb0: chunk row 0 at the sequence's first key; k-step s reads
+    // chunk row 2 s (the lower half-wave) and 2 s + 1 (the upper), kb_step
+    // bytes apart per s; the lane part of an address is a 32-bit byte offset.
+    struct Row {
+      ItemRec rec;
+      int64_t row_tri;
+      int n, ntiles;
+      const char* kb0;
+    };
+    const int64_t kb_step = 2 * a.nb_sum_cap * 16;
+    auto setup = [&](int64_t item) {
+      Row r;
+      r.rec = sld(a.tab.items + item);
+      r.row_tri = static_cast<int64_t>(h) * a.tri_cap + r.rec.tri;
+      r.n = r.rec.i + 1;
+      r.ntiles = (r.n + 31) >> 5;
+      const int64_t tile_b = r.rec.tile - r.rec.i;
+      r.kb0 = reinterpret_cast<const char*>(a.mk) +
+              (static_cast<int64_t>(kvh) * CH * a.nb_sum_cap + tile_b) * 16;
+      return r;
+    };
     // pooled keys of one 32-key tile as MFMA B operands (lane: key 32 tile +
     // l32, dims 16 s + 8 half .. +7; columns past the row's last key read key
     // n - 1: their scores are computed and never stored)
     typename T::vec8 kb[KS];
-    auto load_kb = [&](int tile) {
+    auto load_kb = [&](const Row& r, int tile) {
       int ln = lane;
       asm volatile("" : "+v"(ln));
-      const int j = min(32 * tile + (ln & 31), n - 1);
+      const int j = min(32 * tile + (ln & 31), r.n - 1);
       const uint32_t off = half_off + static_cast<uint32_t>(j) * 16u;
 #pragma unroll
-      for (int s = 0; s < KS; ++s) kb[s] = as_vec8<T>(*reinterpret_cast<const uint4*>(kbase[s] + off));
+      for (int s = 0; s < KS; ++s)
+        kb[s] = as_vec8<T>(*reinterpret_cast<const uint4*>(r.kb0 + s * kb_step + off));
     };
-    // stage the query block in LDS with direct-to-LDS loads (rows past the
-    // sequence end are then zeroed: they still count for j < i); every wave
-    // reads it as MFMA A operands (rows 32*rg + l32, dims 16*s + 8*half .. +7).
-    // The wave's first key tile is loaded in the same wait.
-    {
+    // The query block is staged in LDS with direct-to-LDS loads, and every
+    // wave reads it as MFMA A operands (rows 32*rg + l32, dims 16*s + 8*half
+    // .. +7); the wave's first key tile follows (first_kb). land() waits for
+    // both and zeroes the rows past the sequence end (they still count for
+    // j < i).
+    auto issue_q = [&](const Row& r) {
       TileLanes<D, BLK, 4> tq;
       tq.init(a.qst, __builtin_amdgcn_readfirstlane(w), lane);
-      issue_tile<D, BLK, 4>(sq, a.q + t0 * a.qst + static_cast<int64_t>(h) * a.qhs, a.qst, tq,
-                            i, L, __builtin_amdgcn_readfirstlane(w), lane);
-      if (w < ntiles) load_kb(w);
+      issue_tile<D, BLK, 4>(sq, a.q + r.rec.t0 * a.qst + static_cast<int64_t>(h) * a.qhs, a.qst,
+                            tq, r.rec.i, r.rec.L, __builtin_amdgcn_readfirstlane(w), lane);
+    };
+    auto first_kb = [&](const Row& r) {
+      if (w < r.ntiles) load_kb(r, w);
+    };
+    auto land = [&](const Row& r) {
       asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-      if ((i + 1) * BLK > L) {
+      if ((r.rec.i + 1) * BLK > r.rec.L) {
         for (int cidx = t; cidx < BLK * CH; cidx += 256)
-          if (i * BLK + cidx / CH >= L) sq[cidx] = zero4();
+          if (r.rec.i * BLK + cidx / CH >= r.rec.L) sq[cidx] = zero4();
         __syncthreads();
       }
-    }
-    for (int tile = w; tile < ntiles; tile += 4) {
-      const int j = 32 * tile + l32;
-      const bool jv = j < n;
-      f32x16 acc[RG];
+    };
+    auto score = [&](const Row& r) {
+      const int n = r.n, ntiles = r.ntiles, i = r.rec.i;
+      for (int tile = w; tile < ntiles; tile += 4) {
+        const int j = 32 * tile + l32;
+        const bool jv = j < n;
+        f32x16 acc[RG];
 #pragma unroll
-      for (int rg = 0; rg < RG; ++rg) acc[rg] = f32x16{};
+        for (int rg = 0; rg < RG; ++rg) acc[rg] = f32x16{};
 #pragma unroll
-      for (int s = 0; s < KS; ++s)
+        for (int s = 0; s < KS; ++s)
 #pragma unroll
-        for (int rg = 0; rg < RG; ++rg) {
-          const int r = 32 * rg + l32;
-          const uint4 qop = sq[r * CH + ((2 * s + half) ^ qswz<D>(r))];
-          acc[rg] = T::mfma32(as_vec8<T>(qop), kb[s], acc[rg]);
-        }
+          for (int rg = 0; rg < RG; ++rg) {
+            const int rr = 32 * rg + l32;
+            const uint4 qop = sq[rr * CH + ((2 * s + half) ^ qswz<D>(rr))];
+            acc[rg] = T::mfma32(as_vec8<T>(qop), kb[s], acc[rg]);
+          }
 
-      // the wave's next key tile, loaded as one burst into kb (dead once the
-      // MFMAs above have read it) so that its latency passes behind this
-      // tile's max / exp2 / sum; loads issued between the MFMAs instead
-      // stalled the MFMA stream and measured slower
-      __builtin_amdgcn_sched_barrier(0);
-      if (tile + 4 < ntiles) load_kb(tile + 4);
-      __builtin_amdgcn_sched_barrier(0);
-      // acc[rg][v] = Q[32 rg + 8 (v/4) + 4 half + v%4] . mk[j]
-      float mx = -INFINITY, sum = 0.0f, m;
-#pragma unroll
-      for (int rg = 0; rg < RG; ++rg)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc[rg][v]);
-      if (tile + 1 < ntiles) {  // every column j < i: all BLK rows count
-        m = pair32_max(mx) * c;
+        // the wave's next key tile, loaded as one burst into kb (dead once the
+        // MFMAs above have read it) so that its latency passes behind this
+        // tile's max / exp2 / sum; loads issued between the MFMAs instead
+        // stalled the MFMA stream and measured slower
+        __builtin_amdgcn_sched_barrier(0);
+        if (tile + 4 < ntiles) load_kb(r, tile + 4);
+        __builtin_amdgcn_sched_barrier(0);
+        // acc[rg][v] = Q[32 rg + 8 (v/4) + 4 half + v%4] . mk[j]
+        float mx = -INFINITY, sum = 0.0f, m;
 #pragma unroll
         for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
-          for (int v = 0; v < 16; ++v) sum += __builtin_amdgcn_exp2f(fmaf(acc[rg][v], c, -m));
-      } else {
-        // last tile: j < i all rows, j == i the last row BLK - 1 only
-        // (acc[RG - 1][15] of the upper half-wave), j > i none. The case is
-        // uniform over a lane's values, so the full-tile reduction runs for
-        // every lane and one select per lane picks the result (the same
-        // arithmetic on the rows that count, no per-element masking)
-        const bool full = j < i, rowlast = j == i && half == 1;
-        mx = full ? mx : (rowlast ? acc[RG - 1][15] : -INFINITY);
-        m = pair32_max(mx) * c;
+          for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc[rg][v]);
+        if (tile + 1 < ntiles) {  // every column j < i: all BLK rows count
+          m = pair32_max(mx) * c;
 #pragma unroll
-        for (int rg = 0; rg < RG; ++rg)
+          for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
-          for (int v = 0; v < 16; ++v) sum += __builtin_amdgcn_exp2f(fmaf(acc[rg][v], c, -m));
-        sum = full ? sum
-                   : (rowlast ? __builtin_amdgcn_exp2f(fmaf(acc[RG - 1][15], c, -m)) : 0.0f);
-      }
-      sum = pair32_sum(sum);
-      if (half == 0 && jv) {
-        pl[j] = sum;
-        ml[j] = m;
-        if (a.dump_p) {
-          a.dump_p[row_tri + j] = sum;
-          a.dump_m[row_tri + j] = m;
+            for (int v = 0; v < 16; ++v) sum += __builtin_amdgcn_exp2f(fmaf(acc[rg][v], c, -m));
+        } else {
+          // last tile: j < i all rows, j == i the last row BLK - 1 only
+          // (acc[RG - 1][15] of the upper half-wave), j > i none. The case is
+          // uniform over a lane's values, so the full-tile reduction runs for
+          // every lane and one select per lane picks the result (the same
+          // arithmetic on the rows that count, no per-element masking)
+          const bool full = j < i, rowlast = j == i && half == 1;
+          mx = full ? mx : (rowlast ? acc[RG - 1][15] : -INFINITY);
+          m = pair32_max(mx) * c;
+#pragma unroll
+          for (int rg = 0; rg < RG; ++rg)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) sum += __builtin_amdgcn_exp2f(fmaf(acc[rg][v], c, -m));
+          sum = full ? sum
+                     : (rowlast ? __builtin_amdgcn_exp2f(fmaf(acc[RG - 1][15], c, -m)) : 0.0f);
+        }
+        sum = pair32_sum(sum);
+        if (half == 0 && jv) {
+          pl[j] = sum;
+          ml[j] = m;
+          if (a.dump_p) {
+            a.dump_p[r.row_tri + j] = sum;
+            a.dump_m[r.row_tri + j] = m;
+          }
         }
       }
+      __syncthreads();  // (p, m) complete; every wave is done with the query block
+    };
+
+    const Row ra = setup(item_a);
+    issue_q(ra);
+    first_kb(ra);
+    land(ra);
+    score(ra);
+    // The second row's query-block loads go out before the first row's
+    // selection when that selection can keep its reduction scratch
+    // (select_row's first 104 bytes) in the unused tail of ml instead of the
+    // query block's area; the selection's barriers wait for LDS operations
+    // only, so they do not wait for these loads. (Its first key tile follows
+    // the selection: held across it in registers, it made the kernel spill.)
+    const bool early = item_b >= 0 && ra.n + 32 <= a.nb_max && a.min_budget == 0;
+    Row rb;
+    if (early) {
+      rb = setup(item_b);
+      issue_q(rb);
     }
+    select(ra.rec, item_a, ra.row_tri, early ? static_cast<void*>(ml + a.nb_max - 32) : dyn4);
+    if (item_b < 0) return;
+    if (!early) {
+      lds_barrier();  // the scratch in the query block's area is read to the end
+      rb = setup(item_b);
+      issue_q(rb);
+    }
+    first_kb(rb);
+    land(rb);
+    score(rb);
+    select(rb.rec, item_b, rb.row_tri, dyn4);
   }
-  __syncthreads();
-  int32_t* list = a.idx + row_tri;
-  int32_t* count = a.cnt + static_cast<int64_t>(h) * a.nb_sum_cap + rec.tile;
-  int32_t* row_rec = a.rowrec + 4 * (static_cast<int64_t>(h) * a.nb_sum_cap + item);
-  const int nb = static_cast<int>(sld(a.tab.seq_tile + b + 1) - tile_b);
-  select_row(pl, ml, n, i, nb, a, list, count, row_rec, dyn4);
 }
 
 // fp32 inputs: the same row pipeline with fp32 MFMA (v_mfma_f32_32x32x2_f32,
@@ -498,9 +576,20 @@ hipError_t launch_search_d(const SearchArgs& a, int block, int64_t grid, bool fr
                      : launch_search_t<T, D, 64, false>(a, grid, s);
 }
 
-hipError_t launch_search(const SearchArgs& a, int dtype, int head_dim, int block, int64_t grid,
+// Problems of at least this many (head, row) items score two rows per
+// workgroup (k_search, 16-bit inputs); smaller ones keep one per workgroup,
+// whose grid alone is not much larger than the resident workgroups.
+constexpr int64_t kPairRowsMin = 4096;
+
+hipError_t launch_search(const SearchArgs& args, int dtype, int head_dim, int block, int64_t grid,
                          bool from_scores, hipStream_t s) {
   if (grid <= 0) return hipSuccess;
+  SearchArgs a = args;
+  a.pair_rows = 0;
+  if (dtype != FP_DTYPE_F32 && !from_scores && grid >= kPairRowsMin) {
+    a.pair_rows = 1;
+    grid = static_cast<int64_t>(a.Hq) * ((grid / a.Hq + 1) / 2);  // grid = Hq x item capacity
+  }
   if (dtype == FP_DTYPE_F32) {
     if (from_scores)  // selection only: no input element is read
       return launch_search_d<BF16, 128>(a, block, grid, true, s);
