@@ -77,6 +77,23 @@ def test_native_min_budget(min_budget):
     _check(run_stages(q, k, v, cu, 2048, alpha=0.9, native=True, min_budget=min_budget))
 
 
+@pytest.mark.parametrize("native,min_budget", [(False, 0), (True, 7)])
+def test_paired_rows_odd_item_count(native, min_budget):
+    # 32 heads x 127 rows (at least 4096 items): the search scores two rows
+    # per workgroup (item k with item N-1-k of the heaviest-first order) and
+    # the middle workgroup one; the second row's query block loads during the
+    # first row's selection, or after it with min_budget (whose radix
+    # histogram needs the query block's area) and for rows within 32 blocks
+    # of the longest
+    lens = [8192, 5000, 2900]
+    q, k, v, cu = _rand_inputs(lens, 32, 8, 128, torch.bfloat16, 11, scale=2.0)
+    rows = {0: [(0, 63), (5, 31), (17, 0)], 1: [(3, 39), (30, 20)], 2: [(9, 22), (31, 11)]}
+    rep = run_stages(q, k, v, cu, max(lens), alpha=0.9, native=native, min_budget=min_budget,
+                     attn_rows=rows)
+    assert rep.density < 0.95
+    _check(rep)
+
+
 def test_selection_params_sweep():
     lens = [1024, 700]
     q, k, v, cu = _rand_inputs(lens, 4, 1, 128, torch.bfloat16, 3, scale=2.0)
