@@ -394,19 +394,34 @@ __device__ __forceinline__ bool attn_slot(const Args& a, int slot, int t, Tail t
     }
     return true;
   }
+  // The normalised 32 x D output tile of the wave goes through its own slice
+  // of the K buffer (idle: the last block's S is done, and no K refill
+  // follows it) in the swizzled tile layout, then out as whole rows: 16 bytes
+  // per lane, 64 / CH rows per store instruction. (Stored straight from the
+  // accumulator layout, each instruction wrote 16 bytes into each of 32 rows.)
   const float rcp = 1.0f / l;
-  if (qvalid) {
-    uint16_t* op = a.o + (t0 + qg) * a.ost + static_cast<int64_t>(h) * a.ohs;
+  uint16_t* so = reinterpret_cast<uint16_t*>(sk) + w * (32 * D);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int d = 32 * dt + 8 * g4 + 4 * half;
-        uint2 pk;
-        pk.x = pack2<T>(st.o[dt][4 * g4 + 0] * rcp, st.o[dt][4 * g4 + 1] * rcp);
-        pk.y = pack2<T>(st.o[dt][4 * g4 + 2] * rcp, st.o[dt][4 * g4 + 3] * rcp);
-        *reinterpret_cast<uint2*>(op + d) = pk;
-      }
+    for (int g4 = 0; g4 < 4; ++g4) {
+      uint2 pk;
+      pk.x = pack2<T>(st.o[dt][4 * g4 + 0] * rcp, st.o[dt][4 * g4 + 1] * rcp);
+      pk.y = pack2<T>(st.o[dt][4 * g4 + 2] * rcp, st.o[dt][4 * g4 + 3] * rcp);
+      *reinterpret_cast<uint2*>(so + tile_elem<D>(l32, 32 * dt + 8 * g4 + 4 * half)) = pk;
+    }
+  // lanes read what other lanes of the wave wrote: the wave's LDS operations
+  // run in order; this keeps the compiler from moving the reads above the writes
+  __builtin_amdgcn_wave_barrier();
+  constexpr int RPI = 64 / CH;  // rows per store instruction
+  const int oc = lane % CH;  // the lane's 16-byte chunk of a row
+#pragma unroll
+  for (int k = 0; k < 32 / RPI; ++k) {
+    const int r = RPI * k + lane / CH;  // the wave's query row
+    const uint4 val = *reinterpret_cast<const uint4*>(so + tile_elem<D>(r, 8 * oc));
+    if (i * BLK + 32 * w + r < L)
+      *reinterpret_cast<uint4*>(a.o + (t0 + i * BLK + 32 * w + r) * a.ost +
+                                static_cast<int64_t>(h) * a.ohs + 8 * oc) = val;
   }
   return true;
 }
