@@ -26,6 +26,7 @@ def _check(rep, max_flip_frac=2e-3):
           f"e2e_flips={rep.e2e_flips}/{rep.cells} density={rep.density:.3f} "
           f"out_max={rep.out_max_abs:.2e} out_mean={rep.out_mean_abs:.2e}", flush=True)
     assert rep.pool_ulp <= 1
+    assert rep.pool_bound_violations == 0, rep.notes
     assert rep.m_max_rel < 1e-5
     assert rep.p_max_rel < 1e-4
     assert rep.sel_from_gpu_scores_mismatch == 0

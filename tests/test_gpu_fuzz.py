@@ -82,6 +82,7 @@ def test_random_configuration(seed):
     print(f"  flips={rep.e2e_flips}/{rep.cells} density={rep.density:.3f} "
           f"out_max={rep.out_max_abs:.2e} out_mean={rep.out_mean_abs:.2e}", flush=True)
     assert rep.pool_ulp <= 1
+    assert rep.pool_bound_violations == 0, rep.notes
     assert rep.m_max_rel < 1e-4
     assert rep.p_max_rel < 1e-3
     assert rep.sel_from_gpu_scores_mismatch == 0
@@ -138,6 +139,7 @@ def test_random_large_configuration_persistent_attention(seed):
     print(f"  flips={rep.e2e_flips}/{rep.cells} density={rep.density:.3f} "
           f"out_max={rep.out_max_abs:.2e} out_mean={rep.out_mean_abs:.2e}", flush=True)
     assert rep.pool_ulp <= 1
+    assert rep.pool_bound_violations == 0, rep.notes
     assert rep.m_max_rel < 1e-4
     assert rep.p_max_rel < 1e-3
     assert rep.sel_from_gpu_scores_mismatch == 0

@@ -1,7 +1,9 @@
 """GPU parity of the HIP path against the CPU oracle, stage by stage.
 
 Bars (from the task contract):
-  pooled K           <= 1 ulp of the input dtype (fp32 sum, one rounding)
+  pooled K           <= 1 ulp of the input dtype where the block mean does not
+                     cancel, and everywhere within the fp32 summation bound
+                     ulp + 128 * 2^-24 * mean|k| (fp32 sum, one rounding)
   block scores       fp32 relative error (MFMA accumulation order only)
   selection          EXACT when fed identical fp32 (p, m) -- both directions:
                      GPU scores -> oracle select == GPU select, and
@@ -27,6 +29,7 @@ def _check(rep, max_flip_frac=2e-3):
           f"e2e_flips={rep.e2e_flips}/{rep.cells} density={rep.density:.3f} "
           f"out_max={rep.out_max_abs:.2e} out_mean={rep.out_mean_abs:.2e}", flush=True)
     assert rep.pool_ulp <= 1
+    assert rep.pool_bound_violations == 0, rep.notes
     assert rep.m_max_rel < 1e-4
     assert rep.p_max_rel < 1e-3
     assert rep.sel_from_gpu_scores_mismatch == 0
@@ -92,6 +95,19 @@ def test_paired_rows_odd_item_count(native, min_budget):
                      attn_rows=rows)
     assert rep.density < 0.95
     _check(rep)
+
+
+def test_paired_rows_many_short_sequences():
+    # 64 sequences of at most 16 blocks, 32 heads (over 4096 items): every
+    # workgroup scores two rows, and no row is 32 blocks shorter than the
+    # longest, so the second row's query block always loads after the first
+    # row's selection; ragged lengths with partial blocks and an empty one
+    g = torch.Generator().manual_seed(21)
+    lens = [int(x) for x in torch.randint(1, 2049, (64,), generator=g)]
+    lens[5], lens[17], lens[40] = 0, 2048, 1
+    q, k, v, cu = _rand_inputs(lens, 32, 8, 128, torch.bfloat16, 13, scale=2.0)
+    rows = {1: [(0, 3)], 17: [(31, 15), (6, 0)], 33: [(12, 1)], 63: [(20, 2)]}
+    _check(run_stages(q, k, v, cu, 2048, alpha=0.9, attn_rows=rows))
 
 
 def test_selection_params_sweep():
