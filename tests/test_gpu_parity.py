@@ -97,6 +97,18 @@ def test_paired_rows_odd_item_count(native, min_budget):
     _check(rep)
 
 
+@pytest.mark.parametrize("lens,d,dtype,block", [([16384], 64, torch.bfloat16, 128),
+                                                ([8192, 3000], 64, torch.float16, 64),
+                                                ([6000, 2500], 128, torch.float16, 64)])
+def test_paired_rows_head_dim_dtype_block(lens, d, dtype, block):
+    # the paired-row search (32 heads x at least 128 rows) at head_dim 64, in
+    # fp16 and with 64-token blocks (64-row query blocks, two 32-row groups)
+    q, k, v, cu = _rand_inputs(lens, 32, 8, d, dtype, 17, scale=2.0)
+    last = [(lens[b] + block - 1) // block - 1 for b in range(len(lens))]
+    rows = {b: [(0, last[b]), (13, last[b] // 2), (31, 0)] for b in range(len(lens))}
+    _check(run_stages(q, k, v, cu, max(lens), alpha=0.9, attn_rows=rows, block=block))
+
+
 def test_paired_rows_many_short_sequences():
     # 64 sequences of at most 16 blocks, 32 heads (over 4096 items): every
     # workgroup scores two rows, and no row is 32 blocks shorter than the
