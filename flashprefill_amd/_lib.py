@@ -25,7 +25,7 @@ FP_DTYPE_F16 = 1
 FP_DTYPE_F32 = 2
 FP_STATUS_SEQ_TOO_LONG = 1
 FP_STATUS_BAD_CU_SEQLENS = 2
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 EXPORTS = (
     "fp_workspace_layout", "fp_workspace_bytes", "fp_flashprefill", "fp_plan", "fp_pool_k",

@@ -367,7 +367,7 @@ int scratch_on_current_device(void** out) {
 
 extern "C" {
 
-int fp_abi_version(void) { return 5; }
+int fp_abi_version(void) { return 6; }
 
 const char* fp_last_error(void) { return g_last_error.c_str(); }
 

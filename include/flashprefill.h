@@ -224,7 +224,8 @@ int fp_rope_qk(const fp_rope_args* a, void* stream);
 int fp_read_status(const fp_problem* p, void* workspace, void* stream, uint32_t* status);
 
 const char* fp_last_error(void);
-/* ABI version: bump on any change to fp_problem or fp_ws_layout. */
+/* ABI version: bump on any change to fp_problem, fp_ws_layout or the layout of a
+   workspace region documented above (6: pooled K chunk-major). */
 int fp_abi_version(void);
 
 #ifdef __cplusplus
