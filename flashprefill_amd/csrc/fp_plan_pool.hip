@@ -7,8 +7,9 @@
 //   k_pool  — mean of every K block (block_size tokens) over its valid rows
 //             (ops/flashprefill_native_forward.py:21-67,
 //              ops/flashprefill_varlen_func.py:35-85). HBM-bound: each K byte
-//             is read once with 16-byte loads, sums are kept in fp32 and the
-//             mean is rounded once to the input dtype.
+//             is read once with 16-byte loads, sums are kept in fp64 (exact
+//             for 16-bit inputs whose exponents span fewer than ~38 binades)
+//             and the mean is divided in fp64.
 #include "fp_internal.h"
 
 namespace fp {
@@ -227,9 +228,14 @@ __global__ __launch_bounds__(1024) void k_plan(PlanArgs a) {
 }
 
 // One workgroup per (key block g, kv head hh): 256 threads = R row groups x
-// D / 8 chunks of 16 bytes; each thread sums its rows of one chunk in fp32,
-// the R partial sums are added through LDS in row-group order and the mean is
-// rounded once. Several workgroups per block keep short sequences from
+// D / 8 chunks of 16 bytes; each thread sums its rows of one chunk in fp64,
+// the R partial sums are added through LDS in row-group order, and the mean
+// sum / rows is divided in fp64 and converted to fp32 and then to the input
+// dtype (the rounding path of torch's float64 -> bfloat16 / float16 cast).
+// A 16-bit value has an 8- or 11-bit significand, so a sum of at most 256 of
+// them is exact in fp64 unless their exponents span more than ~38 binades:
+// the mean is then the correctly rounded block mean whatever the order of
+// the additions. Several workgroups per block keep short sequences from
 // running on a handful of CUs. The means are stored chunk-major (16-byte
 // chunk c of key block g and kv head hh at entry g of chunk row hh * C + c),
 // so that the search kernel's loads of 32 consecutive keys' chunk are
@@ -238,7 +244,7 @@ template <typename T, int D>
 __global__ __launch_bounds__(256) void k_pool(PoolArgs a) {
   constexpr int C = D / 8;    // 16-byte chunks per head row
   constexpr int R = 256 / C;  // row groups
-  __shared__ float red[256 * 8];
+  __shared__ double red[256 * 8];
   const int64_t g = blockIdx.x / a.Hkv;
   const int hh = static_cast<int>(blockIdx.x % a.Hkv);
   const int64_t nsum = a.tab.seq_tile[a.B];
@@ -249,28 +255,28 @@ __global__ __launch_bounds__(256) void k_pool(PoolArgs a) {
   const int64_t t0 = a.tab.seq_start[b] + static_cast<int64_t>(i) * a.block;
   const int rows = min(a.block, L - i * a.block);
   const int t = threadIdx.x, c = t % C, rg = t / C;
-  const float inv = 1.0f / static_cast<float>(rows);
   const uint16_t* src = a.k + t0 * a.kst + hh * a.khs + c * 8;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  double acc[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
   for (int r = rg; r < rows; r += R) {
     const uint4 v = ld16(src + static_cast<int64_t>(r) * a.kst);
     const uint16_t* e = reinterpret_cast<const uint16_t*>(&v);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) acc[q] += T::to_f32(e[q]);
+    for (int q = 0; q < 8; ++q) acc[q] += static_cast<double>(T::to_f32(e[q]));
   }
 #pragma unroll
   for (int q = 0; q < 8; ++q) red[t * 8 + q] = acc[q];
   __syncthreads();
   if (rg == 0) {
+    const double n = static_cast<double>(rows);
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      float s = 0.f;
+      double s = 0.0;
       for (int r = 0; r < R; ++r) s += red[(r * C + c) * 8 + q];
       acc[q] = s;
     }
     uint16_t o[8];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) o[q] = T::from_f32(acc[q] * inv);
+    for (int q = 0; q < 8; ++q) o[q] = T::from_f32(static_cast<float>(acc[q] / n));
     // chunk-major: chunk c of (g, hh) is entry g of chunk row hh * C + c
     uint16_t* out = a.mk + ((hh * C + c) * a.nb_sum_cap + g) * 8;
     st16(out, *reinterpret_cast<const uint4*>(o));

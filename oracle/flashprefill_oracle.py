@@ -16,8 +16,11 @@ arithmetic is not reproducible bit-for-bit (Triton's bf16 tree sums, NVIDIA's
 ``ex2.approx``, the reduction order of inductor kernels, autotuned tile
 sizes), the oracle fixes one canonical arithmetic and says so:
 
-* pooled K: fp64 sum of the block's valid rows / n_valid, rounded once to the
-  input dtype (the reference sums in the input dtype, ``…native_forward.py:53``);
+* pooled K: fp64 sum of the block's valid rows / n_valid in fp64, converted to
+  the input dtype by torch's cast (fp64 -> fp32 -> bf16 / fp16, each round to
+  nearest even); the sum of at most 256 16-bit values is exact in fp64 unless
+  their exponents span more than ~38 binades (the reference sums in the input
+  dtype, ``…native_forward.py:53``);
 * dot products: exact (fp64) then rounded once to fp32 (the reference's
   ``tl.dot`` accumulates in fp32 in an unspecified order);
 * ``exp2`` in the normalisation/selection stage: computed in fp64 from the
@@ -30,7 +33,8 @@ sizes), the oracle fixes one canonical arithmetic and says so:
   ``…native_forward.py:298-331`` does.
 
 Pinning status (what checks each function, see ``tests/test_oracle.py``):
-  pool_k            closed form (fp64 block mean) + mutation check
+  pool_k            closed form (fp64 block mean), exact rational mean rounded
+                    to fp64, fp32 then the dtype + mutation check
   block_score       brute-force pure-Python loops on tiny inputs + closed-form
                     diagonal rule (row 127 only) + mutation checks
   normalize_scores  brute-force loops on the formula + invariants
@@ -99,6 +103,8 @@ def pool_k(k_seq: torch.Tensor, block: int = 128) -> torch.Tensor:
 
     k_seq: (S, Hkv, d) one sequence. Returns (NB, Hkv, d) in k_seq.dtype.
     Rows past S do not count (``num_ele`` = number of valid rows, :55-58).
+    The fp64 mean reaches a 16-bit dtype through fp32 (torch's cast rounds
+    fp64 -> fp32 -> bf16 / fp16), a rounding path the GPU kernel repeats.
     """
     S, Hkv, d = k_seq.shape
     nb = num_blocks(S, block)

@@ -3,7 +3,7 @@ bf16), one 262144-token sequence, config 4 (Qwen2.5 shapes, ragged
 {256K, 64K, 17K, 3K, 1K}) and one sequence of the maximum length (1,048,576
 tokens, the search's largest LDS footprint).
 
-Two checks per case:
+Three checks per case:
 * every row's selection: the search kernel's fp32 scores are dumped and the
   oracle's selection from them must equal the GPU's index lists on every
   (head, sequence, q-block) row; for sampled heads the GPU selection fed the
@@ -11,7 +11,11 @@ Two checks per case:
 * sampled rows end to end: the oracle's row pipeline (pooled K of all
   blocks, scores, normalisation, selection, attention) against the GPU's
   lists (threshold flips counted, at most one allowed) and output (bf16
-  tolerance), and two full runs bit-identical."""
+  tolerance), and two full runs bit-identical;
+* every row's output (all cases; the persistent attention grid runs them):
+  the closed form softmax(QK^T / sqrt(d)) V over each row's selected blocks,
+  computed with torch fp32 on the GPU from the kernel's own lists (which the
+  first check pins to the oracle's selection), under the bf16 bars."""
 
 import pytest
 import torch
@@ -19,7 +23,8 @@ import torch
 from flashprefill_amd import synth
 from flashprefill_amd.runtime import FlashPrefillCall
 from oracle import flashprefill_oracle as O
-from tests._parity import OUT_MAX_ABS, OUT_MEAN_ABS, check_every_row_selection
+from tests._parity import (OUT_MAX_ABS, OUT_MEAN_ABS, check_every_row_selection,
+                           every_row_vs_closed_form)
 
 pytestmark = pytest.mark.gpu
 
@@ -71,7 +76,8 @@ def _run_twice(q, k, v, cu, max_len, alpha, block=128):
     return call, outs[0]
 
 
-def _full_case(S, seed, rows, oracle_heads, label, every_row=True, spec=None, block=128):
+def _full_case(S, seed, rows, oracle_heads, label, every_row=True, spec=None, block=128,
+               every_output=True):
     spec = spec or synth.llama_spec(S, seed=seed)
     print(f"\n  {label}: S={S} Hq={spec.num_q_heads} Hkv={spec.num_kv_heads} d={spec.head_dim} "
           f"seed={spec.seed} block={block}", flush=True)
@@ -89,6 +95,18 @@ def _full_case(S, seed, rows, oracle_heads, label, every_row=True, spec=None, bl
     print(f"  {label}: threshold flips {flips}, rows checked {checked}/{len(ref)}", flush=True)
     assert flips <= 1
     assert checked >= len(ref) - 1
+    if every_output:
+        _every_row_output(call, out, label, block)
+
+
+def _every_row_output(call, out, label, block=128):
+    """Every output row against the GPU closed form over the kernel's lists."""
+    mx, mean, rows = every_row_vs_closed_form(call, out, block=block)
+    print(f"  {label}: every row's output vs the closed form: {rows} (head, q-block) rows, "
+          f"max {mx:.2e} mean {mean:.2e}", flush=True)
+    assert rows == call.Hq * sum((n + block - 1) // block for n in call.seq_tables()[3])
+    assert mx <= OUT_MAX_ABS
+    assert mean <= OUT_MEAN_ABS
 
 
 def test_128k_every_row_selection_and_sampled_rows():
@@ -157,3 +175,4 @@ def test_config4_every_row_selection_and_sampled_rows():
     print(f"  config 4: threshold flips {flips}, rows checked {checked}/{total}", flush=True)
     assert flips <= 1
     assert checked >= total - 1
+    _every_row_output(call, o, "config 4")

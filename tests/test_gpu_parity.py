@@ -1,9 +1,8 @@
 """GPU parity of the HIP path against the CPU oracle, stage by stage.
 
 Bars (from the task contract):
-  pooled K           <= 1 ulp of the input dtype where the block mean does not
-                     cancel, and everywhere within the fp32 summation bound
-                     ulp + 128 * 2^-24 * mean|k| (fp32 sum, one rounding)
+  pooled K           <= 1 ulp of the input dtype on every element, and bit
+                     equality for 16-bit inputs (fp64 block sums are exact)
   block scores       fp32 relative error (MFMA accumulation order only)
   selection          EXACT when fed identical fp32 (p, m) -- both directions:
                      GPU scores -> oracle select == GPU select, and
@@ -18,18 +17,18 @@ import pytest
 import torch
 
 from flashprefill_amd import synth
-from tests._parity import OUT_MAX_ABS, OUT_MEAN_ABS, run_stages
+from tests._parity import OUT_MAX_ABS, OUT_MEAN_ABS, assert_pool, run_stages
 
 pytestmark = pytest.mark.gpu
 
 def _check(rep, max_flip_frac=2e-3):
-    print(f"\n  pool_ulp={rep.pool_ulp} m_rel={rep.m_max_rel:.2e} p_rel={rep.p_max_rel:.2e} "
+    print(f"\n  pool_ulp={rep.pool_ulp} pool_mismatch={rep.pool_mismatch} "
+          f"m_rel={rep.m_max_rel:.2e} p_rel={rep.p_max_rel:.2e} "
           f"sel_mismatch(gpu scores)={rep.sel_from_gpu_scores_mismatch} "
           f"sel_mismatch(oracle scores)={rep.sel_from_oracle_scores_mismatch} "
           f"e2e_flips={rep.e2e_flips}/{rep.cells} density={rep.density:.3f} "
           f"out_max={rep.out_max_abs:.2e} out_mean={rep.out_mean_abs:.2e}", flush=True)
-    assert rep.pool_ulp <= 1
-    assert rep.pool_bound_violations == 0, rep.notes
+    assert_pool(rep)
     assert rep.m_max_rel < 1e-4
     assert rep.p_max_rel < 1e-3
     assert rep.sel_from_gpu_scores_mismatch == 0

@@ -6,6 +6,7 @@ error in the oracle's arithmetic.
 """
 
 import math
+from fractions import Fraction
 
 import numpy as np
 import pytest
@@ -48,6 +49,50 @@ def test_pool_k_closed_form(S, block, dtype):
     assert got.dtype == dtype
     # one rounding of the fp64 mean to the storage dtype
     torch.testing.assert_close(got.double(), ref.to(dtype).double(), rtol=0, atol=0)
+
+
+def _bf16_rne_bits(f32: np.ndarray) -> np.ndarray:
+    # round-to-nearest-even of fp32 bit patterns to bf16 (finite inputs)
+    u = f32.astype(np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_pool_k_exact_rational_mean(dtype):
+    # Exact rational block mean (fractions), rounded to fp64, then fp32, then
+    # the 16-bit dtype, each by round to nearest even outside torch. Columns
+    # whose mean cancels to ~0 and one whose mean sits at an fp32 rounding
+    # midpoint are included.
+    g = torch.Generator().manual_seed(8)
+    S, block = 200, 128
+    k = (torch.randn(S, 2, 8, generator=g) * 3).to(dtype)
+    k[:128, 0, 0] = 3.0
+    k[1:128:2, 0, 0] = -3.0
+    k[0, 0, 0] = 3.015625
+    # block mean = M + 2^-27 with M a midpoint between two neighbouring 16-bit
+    # values: fp32 drops the 2^-27, so the cast through fp32 ties to even (M
+    # rounds down to 1.0) where a direct fp64 -> 16-bit rounding rounds up
+    k[:128, 1, 1] = 1.0
+    k[0, 1, 1] = 2.5 if dtype == torch.bfloat16 else 2.0625
+    k[1, 1, 1] = 2.0 ** -20
+    got = O.pool_k(k, block)
+    mid = 1.0 + (2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11)
+    assert got[0, 1, 1].item() == 1.0
+    direct = np.float64(mid + 2.0 ** -27)
+    assert direct > mid  # a direct rounding would give the upper neighbour
+    kv = k.float().numpy().astype(np.float64)
+    for j in range(2):
+        rows = kv[j * block:min(S, (j + 1) * block)]
+        for h in range(2):
+            for x in range(8):
+                mean = sum(Fraction(float(v)) for v in rows[:, h, x]) / len(rows)
+                f32 = np.array([float(mean)], dtype=np.float64).astype(np.float32)
+                if dtype == torch.bfloat16:
+                    want = int(_bf16_rne_bits(f32)[0])
+                else:
+                    want = int(f32.astype(np.float16).view(np.uint16)[0])
+                have = int(got[j, h, x].view(torch.int16).item()) & 0xFFFF
+                assert have == want, (j, h, x, float(mean))
 
 
 def test_pool_k_planted_divisor_mistake():
