@@ -100,10 +100,13 @@ def fused_rope_qk(q: torch.Tensor, k: torch.Tensor, positions: torch.Tensor, the
 
 
 def rms_norm_heads(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """Per-head RMSNorm over the head dim (Qwen3 q_norm / k_norm), fp32 math."""
+    """Per-head RMSNorm over the head dim (Qwen3 q_norm / k_norm,
+    ruler/models/qwen3.py:171-172): fp32 math, the normalised row cast to the
+    input dtype, then multiplied by the weight in that dtype (the composition
+    of transformers' Qwen3MoeRMSNorm, so two roundings)."""
     xf = x.float()
     y = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps)
-    return (y * weight.float()).to(x.dtype)
+    return weight * y.to(x.dtype)
 
 
 class PrefillAttention(torch.nn.Module):

@@ -122,8 +122,12 @@ int layout(const fp_problem* p, fp_ws_layout* L) {
   // block, so with one workgroup per row it outlasts the rest of the attention
   // at short and mid lengths. Rows of more than C = max(8, ceil(NB / 4))
   // blocks run as up to 4 chunks of C blocks; at most min(B, cap / (C + 1))
-  // sequences have more than C blocks. Batches of many long sequences balance
-  // without it (and would need large partial buffers), so it is off there.
+  // sequences have more than C blocks. Each chunk unit keeps fp32 partials
+  // per query head (blk * d + 2 * blk floats), and their region is held to
+  // kSplitPartialBytes: a batch whose units would need more has enough long
+  // rows to balance the attention grid without splitting (one 4K sequence at
+  // 32 heads needs 17 MB; 256 sequences of 4K tokens would need 4.4 GB).
+  constexpr int64_t kSplitPartialBytes = int64_t(64) << 20;
   int64_t split = 0, units = 0;
   if (p->dtype != FP_DTYPE_F32 && p->last_n_block > 0) {
     split = std::max<int64_t>(8, (nb_max + 3) / 4);
@@ -131,7 +135,7 @@ int layout(const fp_problem* p, fp_ws_layout* L) {
       const int64_t seqs = std::min<int64_t>(B, cap / (split + 1));
       const int64_t rows = seqs * std::min<int64_t>(p->last_n_block, nb_max);
       units = rows * ((nb_max + split - 1) / split);
-      if (units * Hq > 65536) units = 0;
+      if (units * Hq * 4 * (blk * d + 2 * blk) > kSplitPartialBytes) units = 0;
     }
     if (units == 0) split = 0;
   }

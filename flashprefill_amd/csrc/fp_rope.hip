@@ -5,7 +5,9 @@
 // ruler/models/qwen3.py:171-176 q_norm / k_norm then RoPE).
 //
 // Per (token t, head h) row of head_dim elements:
-//   [optional] y = round(x * rsqrt(mean(x^2) + eps) * w)        (fp32 math)
+//   [optional] y = round(w * round(x * rsqrt(mean(x^2) + eps)))  (fp32 math;
+//                  the two roundings of Qwen3MoeRMSNorm: the normalised row
+//                  is cast to the input dtype, then multiplied by the weight)
 //   out[k]       = round(y[k] * cos[p][k]    - y[k + d/2] * sin[p][k])
 //   out[k + d/2] = round(y[k + d/2] * cos[p][k] + y[k] * sin[p][k])
 // with p = positions[t] and cos / sin tables of d/2 angles per position
@@ -58,8 +60,10 @@ __global__ __launch_bounds__(256) void k_rope(RopeArgs a) {
       const float inv = rsqrtf(ss / static_cast<float>(D) + a.eps);
 #pragma unroll
       for (int e = 0; e < E; ++e) {
-        x1[e] = T::to_f32(T::from_f32((x1[e] * inv) * T::to_f32(w[E * l + e])));
-        x2[e] = T::to_f32(T::from_f32((x2[e] * inv) * T::to_f32(w[D / 2 + E * l + e])));
+        const float n1 = T::to_f32(T::from_f32(x1[e] * inv));
+        const float n2 = T::to_f32(T::from_f32(x2[e] * inv));
+        x1[e] = T::to_f32(T::from_f32(T::to_f32(w[E * l + e]) * n1));
+        x2[e] = T::to_f32(T::from_f32(T::to_f32(w[D / 2 + E * l + e]) * n2));
       }
     }
     const int64_t p = min(max(a.positions[t], int64_t(0)), a.num_positions - 1);

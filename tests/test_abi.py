@@ -92,6 +92,25 @@ def test_split_row_policy():
     assert rc == _lib.FP_OK and L.split_blocks == 0
 
 
+@pytest.mark.parametrize("B,S,hq,d,block", [(256, 4096, 32, 128, 128), (512, 2048, 32, 128, 128),
+                                            (64, 4096, 28, 128, 64), (4, 4096, 32, 128, 128),
+                                            (1, 4096, 32, 128, 128), (2, 32768, 64, 128, 128),
+                                            (4096, 1024, 32, 64, 64)])
+def test_split_partials_stay_within_their_byte_budget(B, S, hq, d, block):
+    # the chunk partials (fp32 O^T, m, l per unit and query head) are held to
+    # 64 MiB, so batches of many short sequences keep a workspace of tens of MB
+    rc, L = _layout(_problem(batch=B, max_seq_len=S, total_tokens=B * S, num_q_heads=hq,
+                             num_kv_heads=hq // 4, head_dim=d, block_size=block,
+                             q_stride_tok=hq * d, q_stride_head=d, k_stride_tok=hq // 4 * d,
+                             k_stride_head=d, v_stride_tok=hq // 4 * d, v_stride_head=d,
+                             o_stride_tok=hq * d, o_stride_head=d))
+    assert rc == _lib.FP_OK
+    assert L.total_bytes - L.part_off <= 64 << 20
+    assert L.unit_cap * hq * 4 * (block * d + 2 * block) <= 64 << 20
+    if B == 1:
+        assert L.split_blocks > 0  # a single 4K sequence still splits its dense rows
+
+
 @pytest.mark.parametrize("field,value,code", [
     ("dtype", _lib.FP_DTYPE_F32, _lib.FP_E_UNSUPPORTED),
     ("head_dim", 96, _lib.FP_E_UNSUPPORTED),

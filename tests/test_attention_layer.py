@@ -4,6 +4,8 @@ per-head RMSNorm, and the fused QKV projection's views."""
 
 import math
 
+import pytest
+
 import torch
 
 from flashprefill_amd.attention_layer import (PrefillAttention, apply_rope,
@@ -65,3 +67,26 @@ def test_qkv_projection_views_share_storage():
     assert not v.is_contiguous() and v.stride(-1) == 1  # a view into the fused projection
     full = x @ layer.w_qkv.t()
     assert torch.allclose(v.reshape(10, -1), full[:, 6 * 16:])
+
+
+def test_rms_norm_heads_bit_equal_to_transformers_qwen3_moe_rmsnorm():
+    # the reference's Qwen3 attention applies q_norm / k_norm
+    # (ruler/models/qwen3.py:171-172), transformers' Qwen3MoeRMSNorm: the
+    # normalised row is cast to the input dtype before the weight multiply
+    mod = pytest.importorskip("transformers.models.qwen3_moe.modeling_qwen3_moe")
+    g = torch.Generator().manual_seed(4)
+    for dtype in (torch.bfloat16, torch.float16):
+        x = (torch.randn(64, 4, 128, generator=g) * 3).to(dtype)
+        norm = mod.Qwen3MoeRMSNorm(128, eps=1e-6)
+        with torch.no_grad():
+            norm.weight.copy_(torch.rand(128, generator=g) * 2)
+        norm = norm.to(dtype)
+        want = norm(x)
+        got = rms_norm_heads(x, norm.weight.detach(), 1e-6)
+        assert got.dtype == dtype
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+        # one rounding (the weight multiply in fp32) differs on many elements
+        xf = x.float()
+        once = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6) *
+                norm.weight.float()).to(dtype)
+        assert not torch.equal(once, want)

@@ -1,6 +1,7 @@
 """The decoder-layer block's fused q/k RMSNorm + RoPE kernel (fp_rope_qk)
 against the torch composition of the same steps (RMSNorm in fp32 rounded to
-the input dtype, then rotate-half RoPE with fp64-derived fp32 tables), on
+the input dtype, times the weight rounded again as transformers'
+Qwen3MoeRMSNorm does, then rotate-half RoPE with fp64-derived fp32 tables), on
 ragged batches, bf16 and fp16, d 128 and 64, with and without the norms, on
 the strided q / k views of a fused QKV projection. Without the norms the
 result is the same bits. With them the fp32 sum of squares is reduced in
