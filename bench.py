@@ -25,6 +25,7 @@ if ROOT not in sys.path:
 
 METRIC = ("128K prefill attn latency (ms) + effective TFLOPS, speedup vs dense at 1 MI355X")
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_FP32_TFLOPS = 157.3    # MI355X dense fp32 MFMA (config 1 runs fp32 inputs)
 PEAK_HBM_GBPS = 8000.0
 MAX_GFX_MHZ = 2400.0         # MI355X shader clock ceiling (amd-smi gfx max_clk); the bf16 peak is quoted at it
 
@@ -590,8 +591,25 @@ def config1_report(args):
         gpu_call()
         gpu_ms = timed(gpu_call, 20)
         err = (od[0].cpu() - res.out[0]).abs()
-        gpu = {"gpu_ms": gpu_ms, "gpu_effective_tflops": dense_causal_flops(S, Hq, d) /
-               (gpu_ms * 1e-3) / 1e12, "gpu_speedup_vs_cpu": ms / gpu_ms,
+        # the attention stage alone (fp32 MFMA kernel) on the same input in
+        # the batched layout: executed block FLOPs / its time, against the
+        # fp32 MFMA peak
+        from flashprefill_amd.runtime import FlashPrefillCall
+        call = FlashPrefillCall(qd[0], kd[0], vd[0], torch.empty_like(qd[0]), None, S,
+                                alpha=args.alpha, attention_sink=2, window_size=4,
+                                last_n_block=2, native_normalize=True, batch=1,
+                                uniform_seq_len=S)
+        call.run()
+        n_exec = int(call.counts()[:, :nb].sum().item())
+        attn_ms = timed(call.attn, 20)
+        exec_tf = 4.0 * 128 * 128 * d * n_exec / (attn_ms * 1e-3) / 1e12
+        eff_tf = dense_causal_flops(S, Hq, d) / (gpu_ms * 1e-3) / 1e12
+        gpu = {"gpu_ms": gpu_ms, "gpu_effective_tflops": eff_tf,
+               "gpu_effective_frac_of_fp32_mfma_peak": eff_tf / PEAK_FP32_TFLOPS,
+               "gpu_attn_ms": attn_ms, "gpu_executed_tflops": exec_tf,
+               "gpu_attn_frac_of_fp32_mfma_peak": exec_tf / PEAK_FP32_TFLOPS,
+               "fp32_mfma_peak_tflops": PEAK_FP32_TFLOPS,
+               "gpu_speedup_vs_cpu": ms / gpu_ms,
                "gpu_vs_cpu_max_abs_diff": f"{float(err.max()):.3e}", "gpu_dtype": "fp32"}
     return _rounded({**gpu,
         "case": "config 1: 4096 tokens, 8 q / 2 kv heads, d 64, fp32, native forward, alpha "
@@ -607,6 +625,10 @@ def config_cases(config):
     if config == 2:
         return [(synth.llama_spec(S, seed=seed), 0.18, f"{S // 1024}K")
                 for S, seed in ((4096, 4), (16384, 16), (32768, 32))]
+    if config == 3:
+        # config 3's shapes at 262144 tokens: the length of the reference's
+        # 256K headline (README.md:6)
+        return [(synth.llama_spec(262144, seed=256), 0.18, "256K, config 3 shapes")]
     if config == 4:
         return [(synth.qwen_varlen_spec(), 0.08,
                  "ragged {256K, 64K, 17K, 3K, 1K}, Qwen2.5-7B heads")]
@@ -676,14 +698,27 @@ def decoder_layer_report(args):
     nb = S // 128
     n_exec = int(call.counts()[:, :nb].sum().item())
     density = n_exec / (Hq * nb * (nb + 1) // 2)
+    del call
+    # the op inside the block in the three forms of the other configs: times,
+    # executed TFLOP/s and MFMA fraction, search share, and the dense
+    # baselines (own kernel with every block, SDPA flash) at this shape. With
+    # random-init weights the block scores are unstructured and every block
+    # is selected (density 1.0): the op runs dense here.
+    op = measure(q, k, v, cu, [S], alpha, args.steps, args.warmup, not args.no_dense,
+                 dense_reps=1 if args.no_dense else 3)
+    op_keys = ("ms_total", "ms_search", "ms_attn", "ms_plan", "search_share",
+               "search_share_incl_plan", "executed_tflops", "mfma_frac", "effective_tflops",
+               "density", "dense")
     rep = {"report": "config 5", "n_gpus": 1, "dtype": "bf16",
-           "data": "synthetic: hidden states ~ N(0,1), random-init weights (seed 5)",
+           "data": "synthetic: hidden states ~ N(0,1), random-init weights (seed 5); the "
+                   "unstructured scores select every block (density 1.0)",
            "attention_kernel": attn_kernel_name(),
            "config": {"seq_len": S, "hidden": hidden, "num_q_heads": Hq, "num_kv_heads": Hkv,
                       "head_dim": d, "rope_theta": 1e6, "alpha": alpha, "qk_norm": False},
            "ms_layer": ms_layer, "ms_qkv_proj_rope": ms_qkv, "ms_flashprefill": ms_attn,
            "ms_o_proj": ms_oproj, "attention_share": ms_attn / ms_layer, "density": density,
-           "qkv_proj_tflops": 2.0 * S * hidden * (Hq + 2 * Hkv) * d / (ms_qkv * 1e-3) / 1e12}
+           "qkv_proj_tflops": 2.0 * S * hidden * (Hq + 2 * Hkv) * d / (ms_qkv * 1e-3) / 1e12,
+           "op": {kk: op[kk] for kk in op_keys if kk in op}}
     if not args.no_dense:
         from torch.nn.attention import SDPBackend, sdpa_kernel
         qh = q.transpose(0, 1).unsqueeze(0)
@@ -696,6 +731,9 @@ def decoder_layer_report(args):
         rep["ms_dense_attention_sdpa_flash"] = ms_dense
         rep["ms_layer_with_dense_attention"] = ms_layer - ms_attn + ms_dense
         rep["layer_speedup_vs_dense"] = rep["ms_layer_with_dense_attention"] / ms_layer
+        own = op["dense"].get("own_all_blocks_attn_ms")
+        if own:
+            rep["op_speedup_vs_own_dense_kernel"] = own / ms_attn
     return _rounded(rep)
 
 
@@ -865,6 +903,7 @@ def main():
         configs = {}
         for c in (2, 4):
             configs[f"config_{c}"] = config_results(c, sub_steps, sub_warmup, not args.no_dense)
+        configs["config_3_256k"] = config_results(3, sub_steps, sub_warmup, not args.no_dense)
         print("bench: config 5", file=sys.stderr, flush=True)
         sub = argparse.Namespace(steps=sub_steps, warmup=sub_warmup, no_dense=args.no_dense)
         configs["config_5"] = decoder_layer_report(sub)

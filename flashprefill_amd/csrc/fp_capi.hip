@@ -200,7 +200,7 @@ int prepare(const fp_problem* p, void* ws, fp_ws_layout* L) {
   return FP_OK;
 }
 
-int run_plan(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s) {
+fp::PlanArgs plan_args(const fp_problem* p, const fp_ws_layout& L, void* ws) {
   fp::PlanArgs a;
   a.tab = tables(L, ws);
   a.cu = p->cu_seqlens;
@@ -215,11 +215,15 @@ int run_plan(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   a.split_blocks = L.split_blocks;
   a.units = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + L.units_off);
   a.unit_cap = L.unit_cap;
-  const hipError_t e = fp::launch_plan(a, s);
+  return a;
+}
+
+int run_plan(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s) {
+  const hipError_t e = fp::launch_plan(plan_args(p, L, ws), s);
   return e == hipSuccess ? FP_OK : hip_fail(e, "plan launch");
 }
 
-int run_pool(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s) {
+fp::PoolArgs pool_args(const fp_problem* p, const fp_ws_layout& L, void* ws) {
   fp::PoolArgs a;
   a.tab = tables(L, ws);
   a.k = static_cast<const uint16_t*>(p->k);
@@ -230,8 +234,27 @@ int run_pool(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   a.B = p->batch;
   a.Hkv = p->num_kv_heads;
   a.block = p->block_size;
-  const hipError_t e = fp::launch_pool(a, p->dtype, p->head_dim, L.nb_sum_cap, s);
+  return a;
+}
+
+int run_pool(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s) {
+  const hipError_t e = fp::launch_pool(pool_args(p, L, ws), p->dtype, p->head_dim,
+                                       L.nb_sum_cap, s);
   return e == hipSuccess ? FP_OK : hip_fail(e, "pool launch");
+}
+
+// The plan and the pooling of a whole-operator call: one launch (k_plan_pool)
+// for 16-bit inputs and at most kSmallPlanBatch sequences, where the plan's
+// own launch and latency are a visible part of a short call; otherwise k_plan
+// then k_pool.
+int run_plan_and_pool(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s) {
+  if (p->dtype != FP_DTYPE_F32 && p->batch <= fp::kSmallPlanBatch) {
+    const hipError_t e = fp::launch_plan_pool(plan_args(p, L, ws), pool_args(p, L, ws), p->dtype,
+                                              p->head_dim, s);
+    return e == hipSuccess ? FP_OK : hip_fail(e, "plan + pool launch");
+  }
+  const int rc = run_plan(p, L, ws, s);
+  return rc != FP_OK ? rc : run_pool(p, L, ws, s);
 }
 
 fp::SearchArgs search_args(const fp_problem* p, const fp_ws_layout& L, void* ws) {
@@ -430,8 +453,7 @@ int fp_flashprefill(const fp_problem* p, void* ws, void* stream) {
   int rc = prepare(p, ws, &L);
   if (rc != FP_OK) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if ((rc = run_plan(p, L, ws, s)) != FP_OK) return rc;
-  if ((rc = run_pool(p, L, ws, s)) != FP_OK) return rc;
+  if ((rc = run_plan_and_pool(p, L, ws, s)) != FP_OK) return rc;
   if ((rc = run_search(p, L, ws, nullptr, nullptr, nullptr, nullptr, s)) != FP_OK) return rc;
   return run_attn(p, L, ws, s);
 }
@@ -448,8 +470,7 @@ int fp_flashprefill_noalloc(const fp_problem* p, void* stream) {
   void* ws = nullptr;
   if ((rc = scratch_on_current_device(&ws)) != FP_OK) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if ((rc = run_plan(p, L, ws, s)) != FP_OK) return rc;
-  if ((rc = run_pool(p, L, ws, s)) != FP_OK) return rc;
+  if ((rc = run_plan_and_pool(p, L, ws, s)) != FP_OK) return rc;
   if ((rc = run_search(p, L, ws, nullptr, nullptr, nullptr, nullptr, s)) != FP_OK) return rc;
   return run_attn(p, L, ws, s);
 }

@@ -122,6 +122,9 @@ hipError_t launch_plan(const PlanArgs& a, hipStream_t s);
 hipError_t launch_rope(const RopeArgs& a, int dtype, hipStream_t s);
 hipError_t launch_kv_cache_write(const KvCacheArgs& a, hipStream_t s);
 hipError_t launch_pool(const PoolArgs& a, int dtype, int head_dim, int64_t grid, hipStream_t s);
+// k_plan then k_pool as one launch (16-bit inputs, batch <= kSmallPlanBatch)
+hipError_t launch_plan_pool(const PlanArgs& pa, const PoolArgs& a, int dtype, int head_dim,
+                            hipStream_t s);
 hipError_t launch_search(const SearchArgs& a, int dtype, int head_dim, int block, int64_t grid,
                          bool from_scores, hipStream_t s);
 hipError_t launch_attn(const AttnArgs& a, int dtype, int head_dim, int block, int64_t grid,

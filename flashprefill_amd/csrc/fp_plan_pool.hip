@@ -227,33 +227,25 @@ __global__ __launch_bounds__(1024) void k_plan(PlanArgs a) {
   if (t == 0) *tab.status = s_status;
 }
 
-// One workgroup per (key block g, kv head hh): 256 threads = R row groups x
-// D / 8 chunks of 16 bytes; each thread sums its rows of one chunk in fp64,
-// the R partial sums are added through LDS in row-group order, and the mean
-// sum / rows is divided in fp64 and converted to fp32 and then to the input
-// dtype (the rounding path of torch's float64 -> bfloat16 / float16 cast).
-// A 16-bit value has an 8- or 11-bit significand, so a sum of at most 256 of
-// them is exact in fp64 unless their exponents span more than ~38 binades:
-// the mean is then the correctly rounded block mean whatever the order of
-// the additions. Several workgroups per block keep short sequences from
-// running on a handful of CUs. The means are stored chunk-major (16-byte
-// chunk c of key block g and kv head hh at entry g of chunk row hh * C + c),
-// so that the search kernel's loads of 32 consecutive keys' chunk are
-// contiguous.
+// Mean of key block g of kv head hh (rows t0 .. t0 + rows - 1 of K), by one
+// workgroup of 256 threads = R row groups x D / 8 chunks of 16 bytes; each
+// thread sums its rows of one chunk in fp64. The R partial sums are added
+// within each wave by lane exchanges (its 64 / C row groups), then the four
+// waves' sums through LDS, and the mean sum / rows is divided in fp64 and
+// converted to fp32 and then to the input dtype (the rounding path of torch's
+// float64 -> bfloat16 / float16 cast). A 16-bit value has an 8- or 11-bit
+// significand, so a sum of at most 256 of them is exact in fp64 unless their
+// exponents span more than ~38 binades: the mean is then the correctly
+// rounded block mean whatever the order of the additions. The means are
+// stored chunk-major (16-byte chunk c of key block g and kv head hh at entry
+// g of chunk row hh * C + c), so that the search kernel's loads of 32
+// consecutive keys' chunk are contiguous.
 template <typename T, int D>
-__global__ __launch_bounds__(256) void k_pool(PoolArgs a) {
+__device__ __forceinline__ void pool_block(const PoolArgs& a, int64_t g, int hh, int64_t t0,
+                                           int rows) {
   constexpr int C = D / 8;    // 16-byte chunks per head row
   constexpr int R = 256 / C;  // row groups
-  __shared__ double red[256 * 8];
-  const int64_t g = blockIdx.x / a.Hkv;
-  const int hh = static_cast<int>(blockIdx.x % a.Hkv);
-  const int64_t nsum = a.tab.seq_tile[a.B];
-  if (g >= nsum) return;
-  const int b = find_seq(a.tab.seq_tile, a.B, g);
-  const int i = static_cast<int>(g - a.tab.seq_tile[b]);
-  const int L = a.tab.seq_len[b];
-  const int64_t t0 = a.tab.seq_start[b] + static_cast<int64_t>(i) * a.block;
-  const int rows = min(a.block, L - i * a.block);
+  __shared__ double red[3][C][8];  // sums of waves 1 .. 3
   const int t = threadIdx.x, c = t % C, rg = t / C;
   const uint16_t* src = a.k + t0 * a.kst + hh * a.khs + c * 8;
   double acc[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
@@ -263,17 +255,26 @@ __global__ __launch_bounds__(256) void k_pool(PoolArgs a) {
 #pragma unroll
     for (int q = 0; q < 8; ++q) acc[q] += static_cast<double>(T::to_f32(e[q]));
   }
+  // lanes c, c + C, ... of a wave hold the same chunk: xor exchanges over the
+  // lane bits above log2(C) add the wave's row groups
+  const int w = t >> 6;
 #pragma unroll
-  for (int q = 0; q < 8; ++q) red[t * 8 + q] = acc[q];
+  for (int q = 0; q < 8; ++q) {
+    if constexpr (C <= 16) acc[q] += xchg_xor_d<16>(acc[q]);
+    if constexpr (C <= 8) acc[q] += xchg_xor_d<8>(acc[q]);
+    const uint64_t u = __double_as_longlong(acc[q]);
+    const uint32_t lo = xchg32(static_cast<uint32_t>(u)), hi = xchg32(static_cast<uint32_t>(u >> 32));
+    acc[q] += __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+  }
+  if (w > 0 && (t & 63) < C) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) red[w - 1][c][q] = acc[q];
+  }
   __syncthreads();
-  if (rg == 0) {
+  if (t < C) {
     const double n = static_cast<double>(rows);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      double s = 0.0;
-      for (int r = 0; r < R; ++r) s += red[(r * C + c) * 8 + q];
-      acc[q] = s;
-    }
+    for (int q = 0; q < 8; ++q) acc[q] += red[0][c][q] + red[1][c][q] + red[2][c][q];
     uint16_t o[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) o[q] = T::from_f32(static_cast<float>(acc[q] / n));
@@ -281,6 +282,205 @@ __global__ __launch_bounds__(256) void k_pool(PoolArgs a) {
     uint16_t* out = a.mk + ((hh * C + c) * a.nb_sum_cap + g) * 8;
     st16(out, *reinterpret_cast<const uint4*>(o));
   }
+}
+
+// One workgroup per (key block g, kv head hh), the sequence found in the
+// plan's tables. Several workgroups per block keep short sequences from
+// running on a handful of CUs.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void k_pool(PoolArgs a) {
+  const int64_t g = blockIdx.x / a.Hkv;
+  const int hh = static_cast<int>(blockIdx.x % a.Hkv);
+  const int64_t nsum = a.tab.seq_tile[a.B];
+  if (g >= nsum) return;
+  const int b = find_seq(a.tab.seq_tile, a.B, g);
+  const int i = static_cast<int>(g - a.tab.seq_tile[b]);
+  const int L = a.tab.seq_len[b];
+  pool_block<T, D>(a, g, hh, a.tab.seq_start[b] + static_cast<int64_t>(i) * a.block,
+                   min(a.block, L - i * a.block));
+}
+
+// ---------------------------------------------------------------------------
+// Plan and pooling in one launch, for a few sequences
+// ---------------------------------------------------------------------------
+// With at most kSmallPlanBatch sequences every workgroup of the pooling grid
+// derives the sequence table itself: wave 0 applies k_plan's rules (validity,
+// the capacity bound, block and triangle prefix sums, chunk units of the
+// split rows) to cu_seqlens in registers and leaves the table in LDS. The
+// last workgroup writes the plan's tables, work items and unit records; the
+// others pool key block g = blockIdx.x / Hkv of kv head blockIdx.x % Hkv as
+// k_pool does. The plan then costs no launch and no latency of its own ahead
+// of the pooling. Work items are written heaviest first as k_plan orders
+// them, and by sequence within a level.
+struct SmallPlan {
+  int64_t start[kSmallPlanBatch];
+  int64_t tile[kSmallPlanBatch + 1];  // prefix of NB_b
+  int64_t tri[kSmallPlanBatch + 1];   // prefix of NB_b (NB_b + 1) / 2
+  int64_t unit[kSmallPlanBatch + 1];  // prefix of the chunk units
+  int32_t len[kSmallPlanBatch];
+  int32_t nb[kSmallPlanBatch];
+  uint32_t status;
+};
+
+__device__ __forceinline__ int64_t wave_exscan_i64(int64_t v, int64_t* total) {
+  const int lane = threadIdx.x & 63;
+  int64_t x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  *total = __shfl(x, 63);
+  return x - v;
+}
+
+// wave 0: the sequence table of k_plan passes 1 and 2 for B <= 64 sequences
+__device__ void small_plan_table(const PlanArgs& a, SmallPlan& sp) {
+  const int b = threadIdx.x;  // lane
+  int64_t start = 0, end = 0;
+  if (b < a.B) {
+    if (a.cu) {
+      start = a.cu[b];
+      end = a.cu[b + 1];
+    } else {
+      start = static_cast<int64_t>(b) * a.uniform_len;
+      end = start + a.uniform_len;
+    }
+  }
+  // inclusive running maximum of the starts (k_plan's ordering rule)
+  int64_t incl = b < a.B ? start : INT64_MIN;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t y = __shfl_up(incl, o);
+    if (b >= o) incl = max(incl, y);
+  }
+  uint32_t st = 0;
+  int64_t len = 0;
+  if (b < a.B) {
+    len = end - start;
+    if (start < 0 || len < 0 || end > a.total_tokens || incl > start) {
+      st = FP_STATUS_BAD_CU_SEQLENS;
+      len = 0;
+      start = 0;
+    } else if (len > a.max_seq_len) {
+      st = FP_STATUS_SEQ_TOO_LONG;
+      len = 0;
+    }
+  }
+  int64_t nb = (len + a.block - 1) / a.block, nb_tot;
+  wave_exscan_i64(nb, &nb_tot);
+  if (nb_tot > a.nb_sum_cap) {  // as k_plan: skip every sequence
+    len = 0;
+    nb = 0;
+    st |= FP_STATUS_BAD_CU_SEQLENS;
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) st |= __shfl_xor(st, o);
+  const int C = a.split_blocks;
+  int64_t nu = 0;
+  for (int i = max(static_cast<int>(nb) - a.last_n, 0); i < nb; ++i)
+    if (row_is_split(i, static_cast<int>(nb), a.last_n, C)) nu += (i + C) / C;
+  int64_t t1, t2, t3;
+  const int64_t e1 = wave_exscan_i64(nb, &t1);
+  const int64_t e2 = wave_exscan_i64(nb * (nb + 1) / 2, &t2);
+  const int64_t e3 = wave_exscan_i64(nu, &t3);
+  if (b < a.B) {
+    sp.start[b] = start;
+    sp.len[b] = static_cast<int32_t>(len);
+    sp.nb[b] = static_cast<int32_t>(nb);
+    sp.tile[b] = e1;
+    sp.tri[b] = e2;
+    sp.unit[b] = e3;
+  }
+  if (b == 0) {
+    sp.tile[a.B] = t1;
+    sp.tri[a.B] = t2;
+    sp.unit[a.B] = t3;
+    sp.status = st;
+  }
+}
+
+// the last workgroup of k_plan_pool: everything k_plan writes
+__device__ void small_plan_write(const PlanArgs& a, const SmallPlan& sp) {
+  const int t = threadIdx.x, B = a.B;
+  const SeqTables& tab = a.tab;
+  if (t < B) {
+    tab.seq_start[t] = sp.start[t];
+    tab.seq_len[t] = sp.len[t];
+    tab.seq_tile[t] = sp.tile[t];
+    tab.seq_tri[t] = sp.tri[t];
+  }
+  if (t == 0) {
+    tab.seq_tile[B] = sp.tile[B];
+    tab.seq_tri[B] = sp.tri[B];
+    *tab.status = sp.status;
+    a.units[0] = static_cast<int32_t>(min(sp.unit[B], a.unit_cap));
+  }
+  if (t < kQueueWords) a.units[kQueueOff + t] = 0;  // empty attention work queues
+  // work items: item (b, i) goes after every item of a higher level and
+  // after the items of level i of the sequences before b
+  const int64_t nsum = sp.tile[B];
+  for (int64_t g = t; g < nsum; g += blockDim.x) {
+    int b = 0;
+    while (b + 1 < B && sp.tile[b + 1] <= g) ++b;
+    const int i = static_cast<int>(g - sp.tile[b]);
+    int64_t pos = 0;
+    for (int x = 0; x < B; ++x) {
+      pos += max(sp.nb[x] - 1 - i, 0);
+      if (x < b && sp.nb[x] > i) ++pos;
+    }
+    ItemRec r;
+    r.b = b;
+    r.i = i;
+    r.L = sp.len[b];
+    r.tile = static_cast<int32_t>(g);
+    r.t0 = sp.start[b];
+    r.tri = sp.tri[b] + static_cast<int64_t>(i) * (i + 1) / 2;
+    tab.items[pos] = r;
+  }
+  // chunk units of the split rows, numbered as k_plan numbers them
+  if (t < B) {
+    UnitRec* urec = reinterpret_cast<UnitRec*>(reinterpret_cast<char*>(a.units) + 64);
+    const int C = a.split_blocks, nb = sp.nb[t];
+    int64_t u = sp.unit[t];
+    for (int i = max(nb - a.last_n, 0); i < nb; ++i) {
+      if (!row_is_split(i, nb, a.last_n, C)) continue;
+      const int nc = (i + C) / C;
+      for (int c = 0; c < nc; ++c, ++u) {
+        if (u >= a.unit_cap) continue;  // the host bound makes this unreachable
+        UnitRec ur;
+        ur.r.b = t;
+        ur.r.i = i;
+        ur.r.L = sp.len[t];
+        ur.r.tile = static_cast<int32_t>(sp.tile[t] + i);
+        ur.r.t0 = sp.start[t];
+        ur.r.tri = sp.tri[t] + static_cast<int64_t>(i) * (i + 1) / 2;
+        ur.c = c;
+        ur.nc = nc;
+        ur.pad[0] = ur.pad[1] = 0;
+        urec[u] = ur;
+      }
+    }
+  }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void k_plan_pool(PlanArgs pa, PoolArgs a) {
+  __shared__ SmallPlan sp;
+  if (threadIdx.x < 64) small_plan_table(pa, sp);
+  __syncthreads();
+  if (blockIdx.x == gridDim.x - 1) {
+    small_plan_write(pa, sp);
+    return;
+  }
+  const int64_t g = blockIdx.x / a.Hkv;
+  const int hh = static_cast<int>(blockIdx.x % a.Hkv);
+  if (g >= sp.tile[a.B]) return;
+  int b = 0;
+  while (b + 1 < a.B && sp.tile[b + 1] <= g) ++b;
+  const int i = static_cast<int>(g - sp.tile[b]);
+  pool_block<T, D>(a, g, hh, sp.start[b] + static_cast<int64_t>(i) * a.block,
+                   min(a.block, sp.len[b] - i * a.block));
 }
 
 // fp32 keys: the block mean summed in fp64 (in row order) and rounded once to
@@ -316,6 +516,20 @@ hipError_t launch_plan(const PlanArgs& a, hipStream_t s) {
   // for the item scatter
   const int threads = a.B <= 256 && a.nb_max <= 256 ? 256 : 1024;
   hipLaunchKernelGGL(k_plan, dim3(1), dim3(threads), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_plan_pool(const PlanArgs& pa, const PoolArgs& a, int dtype, int head_dim,
+                            hipStream_t s) {
+  // one workgroup per (key block, kv head) of the capacity, plus the table writer
+  const dim3 g(static_cast<unsigned>(a.nb_sum_cap * a.Hkv + 1)), blk(256);
+  if (dtype == FP_DTYPE_BF16) {
+    if (head_dim == 128) hipLaunchKernelGGL((k_plan_pool<BF16, 128>), g, blk, 0, s, pa, a);
+    else hipLaunchKernelGGL((k_plan_pool<BF16, 64>), g, blk, 0, s, pa, a);
+  } else {
+    if (head_dim == 128) hipLaunchKernelGGL((k_plan_pool<F16, 128>), g, blk, 0, s, pa, a);
+    else hipLaunchKernelGGL((k_plan_pool<F16, 64>), g, blk, 0, s, pa, a);
+  }
   return hipGetLastError();
 }
 
