@@ -244,6 +244,100 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
   }
 }
 
+// Flash-decoding merge of a split row's chunk partials into its output rows:
+// m = max_c m_c, w_c = exp2(m_c - m), O = sum_c w_c acc_c / sum_c w_c l_c,
+// with the chunks taken in order (the arithmetic of k_merge, so either path
+// gives the same bits). Threads: nt / BLK per query row (2 at BLK = 128 and
+// 64), each D / 2 dims in groups of 16; each round issues all of a group
+// pair's loads before using them.
+template <typename T, int D, int BLK, typename Args>
+__device__ __forceinline__ void merge_row(const Args& a, int h, int u0, int nc,
+                                          const ItemRec& rec, int t) {
+  constexpr int MAXC = 4;          // chunks per split row (host policy)
+  constexpr int NT = 2 * BLK;      // threads of the workgroup
+  constexpr int TPR = NT / BLK;    // threads per query row
+  constexpr int XT = D / TPR;      // dims per thread
+  constexpr int GP = 32;           // dims per round
+  const int r = t / TPR;
+  const int qg = rec.i * BLK + r;
+  if (qg >= rec.L) return;
+  nc = min(nc, MAXC);
+  const int64_t S = BLK * D + 2 * BLK;  // floats per partial
+  const float* p0 = a.part + (static_cast<int64_t>(h) * a.unit_cap + u0) * S;
+  float mc[MAXC], lc[MAXC];
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    mc[c] = c < nc ? p0[c * S + BLK * D + r] : -INFINITY;
+    lc[c] = c < nc ? p0[c * S + BLK * D + BLK + r] : 0.0f;
+  }
+  float m = mc[0];
+#pragma unroll
+  for (int c = 1; c < MAXC; ++c) m = fmaxf(m, mc[c]);
+  float wc[MAXC], lsum = 0.0f;
+#pragma unroll
+  for (int c = 0; c < MAXC; ++c) {
+    wc[c] = c < nc ? __builtin_amdgcn_exp2f(mc[c] - m) : 0.0f;
+    lsum += wc[c] * lc[c];
+  }
+  const float rcp = 1.0f / lsum;
+  const int xb = XT * (t % TPR);
+  uint16_t* op = a.o + (rec.t0 + qg) * a.ost + static_cast<int64_t>(h) * a.ohs + xb;
+#pragma unroll 1
+  for (int x0 = 0; x0 < XT; x0 += GP) {
+    float4 oc[MAXC][GP / 4];
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c)
+#pragma unroll
+      for (int q = 0; q < GP / 4; ++q)
+        oc[c][q] = c < nc ? *reinterpret_cast<const float4*>(
+                                p0 + c * S + static_cast<int64_t>(r) * D + xb + x0 + 4 * q)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int q = 0; q < GP / 4; ++q) {
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int c = 0; c < MAXC; ++c) {
+        acc.x += wc[c] * oc[c][q].x;
+        acc.y += wc[c] * oc[c][q].y;
+        acc.z += wc[c] * oc[c][q].z;
+        acc.w += wc[c] * oc[c][q].w;
+      }
+      uint2 pk;
+      pk.x = pack2<T>(acc.x * rcp, acc.y * rcp);
+      pk.y = pack2<T>(acc.z * rcp, acc.w * rcp);
+      *reinterpret_cast<uint2*>(op + x0 + 4 * q) = pk;
+    }
+  }
+}
+
+// Arrival of one chunk of a split row (its partials stored by every thread):
+// the chunk that completes the row's count merges it. All chunks of a row
+// run on one XCD (AttnArgs::merge_inline), so they share its L2. Release:
+// every thread waits until its stores are done (in L2), then the workgroup
+// barrier, then one atomic increment (performed in L2). Acquire, by the last
+// chunk: after the atomic returns, this CU's L1 is invalidated, so the other
+// chunks' partials are read from L2. (These are the instructions the
+// compiler emits for a workgroup-scope release / acquire when a workgroup's
+// waves may sit on different CUs of one L2.)
+template <typename T, int D, int BLK, typename Args>
+__device__ __forceinline__ void merge_if_last(const Args& a, int h, int u0, int nc,
+                                              const ItemRec& rec, int t) {
+  __shared__ int s_last;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (t == 0) {
+    int32_t* cnt = a.arrivals + static_cast<int64_t>(h) * a.unit_cap + u0;
+    s_last = atomicAdd(cnt, 1) == nc - 1;
+    // every chunk of the row has arrived: re-arm the counter, so that an
+    // attention launch repeated on the same plan starts from zero as well
+    if (s_last) atomicExch(cnt, 0);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  asm volatile("buffer_inv sc0" ::: "memory");
+  merge_row<T, D, BLK>(a, h, u0, nc, rec, t);
+}
+
 // One work slot of the attention grid: a chunk unit (slot < unit_slots) or
 // a row. Every wave returns together (the early returns depend on the slot
 // only). The K and V buffers are the workgroup's static LDS. `tail()` runs
@@ -357,7 +451,10 @@ __device__ __forceinline__ bool attn_slot(const Args& a, int slot, int t, Tail t
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) st.o[dt] = f32x16{};
   st.m_run = -INFINITY;
-  st.l_part = half == 0 ? 1.0f : 0.0f;  // the two halves' partial sums add up to l
+  // the two halves' partial sums add up to l: a row starts from the
+  // reference's l = 1.0 (cleared by its first block's rescale, alpha =
+  // exp2(-inf) = 0), a chunk of a split row from l = 0
+  st.l_part = half == 0 && unit < 0 ? 1.0f : 0.0f;
 
   const uint16_t* sv16 = reinterpret_cast<const uint16_t*>(sv);
   const int nplain = ncnt - (has_diag ? 1 : 0);
@@ -391,6 +488,12 @@ __device__ __forceinline__ bool attn_slot(const Args& a, int slot, int t, Tail t
     if (half == 0) {
       pp[BLK * D + qrow] = st.m_run;
       pp[BLK * D + BLK + qrow] = l;
+    }
+    if (a.merge_inline) {
+      // the unit record is read again rather than kept live across the block loop
+      const UnitRec ur = sld(
+          reinterpret_cast<const UnitRec*>(reinterpret_cast<const char*>(a.units) + 64) + unit);
+      merge_if_last<T, D, BLK>(a, h, unit - ur.c, ur.nc, ur.r, t);
     }
     return true;
   }

@@ -141,7 +141,9 @@ int layout(const fp_problem* p, fp_ws_layout* L) {
   }
   L->split_blocks = static_cast<int32_t>(split);
   L->unit_cap = units;
-  L->units_off = off;      off = align_up(off + 64 + sizeof(fp::UnitRec) * units);
+  // units region: count and queue words, the unit records, then one arrival
+  // counter per (head, unit) for the split rows merged inside the attention
+  L->units_off = off;      off = align_up(off + 64 + sizeof(fp::UnitRec) * units + 4 * Hq * units);
   L->part_off = off;       off = align_up(off + 4 * Hq * units * (blk * d + 2 * blk));
   L->total_bytes = off;
   return FP_OK;
@@ -200,6 +202,12 @@ int prepare(const fp_problem* p, void* ws, fp_ws_layout* L) {
   return FP_OK;
 }
 
+int32_t* arrival_counters(const fp_problem* p, const fp_ws_layout& L, void* ws) {
+  (void)p;
+  return reinterpret_cast<int32_t*>(static_cast<char*>(ws) + L.units_off + 64 +
+                                    sizeof(fp::UnitRec) * L.unit_cap);
+}
+
 fp::PlanArgs plan_args(const fp_problem* p, const fp_ws_layout& L, void* ws) {
   fp::PlanArgs a;
   a.tab = tables(L, ws);
@@ -215,6 +223,8 @@ fp::PlanArgs plan_args(const fp_problem* p, const fp_ws_layout& L, void* ws) {
   a.split_blocks = L.split_blocks;
   a.units = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + L.units_off);
   a.unit_cap = L.unit_cap;
+  a.arrivals = arrival_counters(p, L, ws);
+  a.n_arrivals = static_cast<int64_t>(p->num_q_heads) * L.unit_cap;
   return a;
 }
 
@@ -333,6 +343,13 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   a.unit_slots = (static_cast<int64_t>(p->num_q_heads) * L.unit_cap + 7) / 8 * 8;
   a.total_slots = a.unit_slots + fp::attn_grid(p->num_q_heads, p->num_kv_heads, L.nb_sum_cap);
   a.queue = reinterpret_cast<int32_t*>(base + L.units_off) + fp::kQueueOff;
+  // The chunks of a split row combine their partials themselves (the last to
+  // finish reads the others' from L2) when they all run on one XCD: with Hq a
+  // multiple of 8 the unit slots of head h are the slots of XCD h / (Hq / 8)
+  // (map_item), which share one L2. Otherwise k_merge runs after the
+  // attention.
+  a.arrivals = arrival_counters(p, L, ws);
+  a.merge_inline = p->num_q_heads % 8 == 0 ? 1 : 0;
   hipError_t e;
   if (p->dtype == FP_DTYPE_F32) {
     e = fp::launch_attn_f32(a, p->head_dim, p->block_size, a.total_slots, s);
@@ -350,7 +367,7 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
     const int64_t grid = persist ? resident : a.total_slots;
     e = fp::launch_attn(a, p->dtype, p->head_dim, p->block_size, grid, persist, s);
   }
-  if (e == hipSuccess && L.split_blocks > 0)
+  if (e == hipSuccess && L.split_blocks > 0 && !a.merge_inline)
     e = fp::launch_merge(a, p->dtype, p->head_dim, p->block_size, s);
   return e == hipSuccess ? FP_OK : hip_fail(e, "attention launch");
 }

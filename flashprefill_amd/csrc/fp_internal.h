@@ -21,6 +21,8 @@ struct PlanArgs {
   int32_t split_blocks;  // blocks per chunk of a split row (0: none)
   int32_t* units;      // chunk units: count at [0], queue words, records from byte 64
   int64_t unit_cap;
+  int32_t* arrivals;   // per (head, unit) arrival counters of the split rows, zeroed here
+  int64_t n_arrivals;
 };
 
 struct PoolArgs {
@@ -83,6 +85,11 @@ struct AttnArgs {
   // x, x + 8, x + 16, ... < total_slots from queue[x] (queue = units + kQueueOff)
   int32_t* queue;
   int64_t total_slots;
+  // merge_inline: the last chunk of a split row to finish combines the row's
+  // partials (counted in arrivals[h * unit_cap + first unit of the row]);
+  // otherwise k_merge does
+  int32_t* arrivals;
+  int32_t merge_inline;
 };
 
 struct KvCacheArgs {

@@ -186,6 +186,7 @@ __global__ __launch_bounds__(1024) void k_plan(PlanArgs a) {
     a.units[0] = static_cast<int32_t>(min(carry_unit, a.unit_cap));
   }
   if (t < kQueueWords) a.units[kQueueOff + t] = 0;  // empty attention work queues
+  for (int64_t x = t; x < a.n_arrivals; x += nt) a.arrivals[x] = 0;
   __syncthreads();
 
   // 3. level sizes c_i = #{b : NB_b > i} (suffix sum of the histogram), then
@@ -417,6 +418,7 @@ __device__ void small_plan_write(const PlanArgs& a, const SmallPlan& sp) {
     a.units[0] = static_cast<int32_t>(min(sp.unit[B], a.unit_cap));
   }
   if (t < kQueueWords) a.units[kQueueOff + t] = 0;  // empty attention work queues
+  for (int64_t x = t; x < a.n_arrivals; x += blockDim.x) a.arrivals[x] = 0;
   // work items: item (b, i) goes after every item of a higher level and
   // after the items of level i of the sequences before b
   const int64_t nsum = sp.tile[B];
