@@ -1,8 +1,15 @@
 """vLLM attention-backend hook: FlashPrefill for prefill steps.
 
-Mirrors what the reference's vLLM patch does to
-``FlashAttentionImpl.forward`` (``patches/patch_loader_vllm_0_12_0.py:57-253``,
-and the 0.10 variant ``patches/patch_loader_vllm_0_10_0.py``):
+Two forwards, one per reference patch:
+
+* ``make_forward`` / ``apply_patch``: vLLM's v1 engine
+  (``patches/patch_loader_vllm_0_12_0.py:57-253``), described below;
+* ``make_forward_v0`` / ``apply_patch_v0``: the v0 engine's backend
+  (``patches/patch_loader_vllm_0_10_0.py:55-376``), whose metadata splits a
+  batch into prefill tokens first and decode tokens after them.
+
+The v1 forward mirrors what the 0.12 patch does to
+``FlashAttentionImpl.forward``:
 
 * write the step's key / value rows into the paged KV cache
   (``reshape_and_cache_flash``, :140-149) -- here the HIP kernel behind
@@ -217,4 +224,118 @@ def apply_patch(impl_cls=None, config: str = DEFAULT_CONFIG, ops: Optional[HookO
             pass
     original = impl_cls.forward
     impl_cls.forward = make_forward(cfg, ops)
+    return original
+
+
+# ---------------------------------------------------------------------------
+# vLLM v0 engine (patches/patch_loader_vllm_0_10_0.py)
+# ---------------------------------------------------------------------------
+
+def _is_decoder(attn_type) -> bool:
+    name = str(getattr(attn_type, "value", attn_type)).lower().rsplit(".", 1)[-1]
+    return name == "decoder"
+
+
+def make_forward_v0(cfg: Dict[str, Any], ops: Optional[HookOps] = None):
+    """The v0 engine's FlashAttentionImpl.forward replacement
+    (patches/patch_loader_vllm_0_10_0.py:78-376), closed over ``cfg``:
+
+    * the step's key / value rows go into the paged cache at ``slot_mapping``
+      when the cache is allocated (:139-172); fp8 caches are rejected;
+    * the batch's first ``num_prefill_tokens`` query rows are prefill, the
+      ``num_decode_tokens`` after them decode (:186-195);
+    * prefill without block tables (or with an empty cache) is FlashPrefill
+      over the step's own rows, cu_seqlens = ``seq_start_loc`` and
+      max_seq_len = ``max_prefill_seq_len`` (:197-246); prefill with block
+      tables (prefix caching) is paged attention over the cache, queries
+      ending at ``seq_lens_tensor`` (:270-295), ``ops.decode``'s operation;
+    * decode is paged attention over the cache: varlen with
+      ``query_start_loc`` when ``max_decode_query_len > 1`` (:313-339), one
+      query per sequence otherwise (:340-368).
+
+    Attention types other than decoder go to ``ops.encoder``, cache write
+    included (the reference writes encoder-decoder layers through
+    ``cross_slot_mapping`` and then runs them through the same causal
+    FlashPrefill call, which only suits decoder layers); fused output
+    quantisation is rejected (:108-111)."""
+    ops = ops or HookOps()
+
+    def flash_prefill_forward_v0(self, layer, query, key, value, kv_cache, attn_metadata,
+                                 output=None, output_scale=None):
+        if output is None:
+            raise ValueError("Output tensor must be provided.")
+        if output_scale is not None:
+            raise NotImplementedError("fused output quantization is not supported")
+        attn_type = getattr(self, "attn_type", "decoder")
+        if not _is_decoder(attn_type):
+            if ops.encoder is None:
+                raise NotImplementedError("encoder and encoder-decoder attention are left to "
+                                          "vLLM's backend")
+            return ops.encoder(self, query, key, value, output, attn_metadata, layer)
+        fp8 = str(getattr(self, "kv_cache_dtype", "auto")).startswith("fp8")
+        if fp8:
+            raise NotImplementedError("fp8 KV caches are not supported by this hook")
+        scale = getattr(self, "scale", 1.0 / math.sqrt(query.shape[-1]))
+        key_cache = value_cache = None
+        if kv_cache.numel() > 0:
+            key_cache, value_cache = kv_cache[0], kv_cache[1]
+            if key is not None and value is not None:
+                ops.cache_write(key, value, key_cache, value_cache,
+                                attn_metadata.slot_mapping.flatten())
+        n_pre = attn_metadata.num_prefill_tokens
+        n_dec = attn_metadata.num_decode_tokens
+        prefill_meta = attn_metadata.prefill_metadata
+        if prefill_meta is not None:
+            tables = getattr(prefill_meta, "block_tables", None)
+            if kv_cache.numel() == 0 or tables is None or tables.numel() == 0:
+                ops.prefill(query[:n_pre], key[:n_pre], value[:n_pre], output[:n_pre],
+                            prefill_meta.seq_start_loc, prefill_meta.max_prefill_seq_len,
+                            cfg["alpha"], cfg["block_size"], cfg["attention_sink"],
+                            cfg["window_size"], cfg["last_n_full_block"])
+            else:  # prefix caching: the new queries end each cached sequence
+                ops.decode(query[:n_pre], key_cache, value_cache, output[:n_pre],
+                           prefill_meta.query_start_loc, prefill_meta.seq_lens_tensor, tables,
+                           scale)
+        decode_meta = attn_metadata.decode_metadata
+        if decode_meta is not None:
+            dq = query[n_pre:n_pre + n_dec]
+            dout = output[n_pre:n_pre + n_dec]
+            if (decode_meta.max_decode_query_len or 1) > 1:
+                cu = decode_meta.query_start_loc
+            else:  # one query per sequence
+                cu = torch.arange(decode_meta.seq_lens_tensor.numel() + 1, dtype=torch.int32,
+                                  device=query.device)
+            ops.decode(dq, key_cache, value_cache, dout, cu, decode_meta.seq_lens_tensor,
+                       decode_meta.block_tables, scale)
+        return output
+
+    return flash_prefill_forward_v0
+
+
+def apply_patch_v0(impl_cls=None, config: str = DEFAULT_CONFIG, ops: Optional[HookOps] = None):
+    """Replace ``impl_cls.forward`` (default: the v0 engine's
+    FlashAttentionImpl, imported from either module path the reference tries,
+    patch_loader_vllm_0_10_0.py:57-61) with the v0 FlashPrefill forward for
+    ``config``; returns the original forward."""
+    if impl_cls is None:
+        try:
+            import vllm.attention.backends.flash_attn as fa_backend  # noqa: WPS433
+        except ImportError:
+            import vllm.model_executor.layers.attention.backends.flash_attn as fa_backend  # noqa
+        impl_cls = fa_backend.FlashAttentionImpl
+    if ops is None:
+        ops = HookOps()
+        try:  # inside vLLM, paged attention is vLLM's own op (patch :19-20, :270-368)
+            from vllm.vllm_flash_attn import flash_attn_varlen_func as vllm_fa
+
+            def vllm_paged(q, kc, vc, out, cu, seqused_k, block_table, scale):
+                max_q = int((cu[1:] - cu[:-1]).max())
+                vllm_fa(q=q, k=kc, v=vc, out=out, cu_seqlens_q=cu, max_seqlen_q=max_q,
+                        seqused_k=seqused_k, max_seqlen_k=int(seqused_k.max()),
+                        softmax_scale=scale, causal=True, block_table=block_table)
+            ops.decode = vllm_paged
+        except ImportError:
+            pass
+    original = impl_cls.forward
+    impl_cls.forward = make_forward_v0(ATTENTION_CONFIGS[config], ops)
     return original

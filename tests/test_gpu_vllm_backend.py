@@ -116,3 +116,68 @@ def test_prefill_then_decode_through_the_hooked_forward():
             s = ks[:, h // (Hq // Hkv)] @ qd[b, h].float() / math.sqrt(d)
             o = torch.softmax(s, 0) @ vs[:, h // (Hq // Hkv)]
             assert (out_d[b, h].float() - o).abs().max().item() <= 2e-2
+
+
+def test_v0_mixed_step_prefill_rows_then_decode_rows():
+    # the v0 engine's batch: prefill tokens of two new sequences first, then
+    # one decode token of each of two sequences already in the cache
+    g = torch.Generator().manual_seed(3)
+    Hq, Hkv, d, bs, nblk = 8, 2, 128, 16, 120
+    pre = [600, 257]
+    old = [300, 90]  # cached lengths of the decoding sequences (without the new token)
+    P, Dn = sum(pre), len(old)
+    perm = torch.randperm(nblk, generator=g).tolist()
+    need = [(n + bs - 1) // bs for n in pre] + [(n + 1 + bs - 1) // bs for n in old]
+    table = torch.zeros(len(need), max(need), dtype=torch.int32)
+    pos = 0
+    for r, m in enumerate(need):
+        table[r, :m] = torch.tensor(perm[pos:pos + m])
+        pos += m
+    table = table.to(DEV)
+
+    def slot(r, p):
+        return int(table[r, p // bs]) * bs + p % bs
+
+    kv = torch.zeros(2, nblk, bs, Hkv, d, dtype=torch.bfloat16, device=DEV)
+    # earlier tokens of the decoding sequences, already cached
+    hist_k = [(torch.randn(n, Hkv, d, generator=g) * 1.5).to(torch.bfloat16).to(DEV) for n in old]
+    hist_v = [torch.randn(n, Hkv, d, generator=g).to(torch.bfloat16).to(DEV) for n in old]
+    for j, n in enumerate(old):
+        for p in range(n):
+            s = slot(2 + j, p)
+            kv[0, s // bs, s % bs] = hist_k[j][p]
+            kv[1, s // bs, s % bs] = hist_v[j][p]
+    T = P + Dn
+    q = (torch.randn(T, Hq, d, generator=g) * 1.5).to(torch.bfloat16).to(DEV)
+    k = (torch.randn(T, Hkv, d, generator=g) * 1.5).to(torch.bfloat16).to(DEV)
+    v = torch.randn(T, Hkv, d, generator=g).to(torch.bfloat16).to(DEV)
+    slots = [slot(0, p) for p in range(pre[0])] + [slot(1, p) for p in range(pre[1])] + \
+        [slot(2 + j, n) for j, n in enumerate(old)]
+    cu = torch.tensor([0, pre[0], P], dtype=torch.int32, device=DEV)
+    pm = SimpleNamespace(seq_start_loc=cu, max_prefill_seq_len=max(pre), query_start_loc=cu,
+                         seq_lens_tensor=torch.tensor(pre, device=DEV), block_tables=None)
+    dm = SimpleNamespace(seq_lens_tensor=torch.tensor([n + 1 for n in old], device=DEV),
+                         max_decode_query_len=1, query_start_loc=None,
+                         block_tables=table[2:])
+    meta = SimpleNamespace(num_prefill_tokens=P, num_decode_tokens=Dn,
+                           slot_mapping=torch.tensor(slots, device=DEV),
+                           prefill_metadata=pm, decode_metadata=dm)
+    impl = SimpleNamespace(attn_type="decoder", kv_cache_dtype="auto", scale=1 / math.sqrt(d))
+    fwd = vb.make_forward_v0(vb.ATTENTION_CONFIGS["flashprefill_qwen2"])
+    out = torch.full((T, Hq, d), 5.0, dtype=torch.bfloat16, device=DEV)
+    assert fwd(impl, None, q, k, v, kv, meta, output=out) is out
+    want = torch.empty(P, Hq, d, dtype=torch.bfloat16, device=DEV)
+    flash_prefill_varlen_func(q[:P], k[:P], v[:P], want, cu, max(pre), 0.08, 128, 2, 4, 2)
+    torch.cuda.synchronize()
+    assert torch.equal(out[:P], want)
+    for t in (0, pre[0] - 1, pre[0], P - 1):  # prefill rows reached the cache
+        s = slots[t]
+        assert torch.equal(kv[0, s // bs, s % bs], k[t]) and torch.equal(kv[1, s // bs, s % bs], v[t])
+    G = Hq // Hkv
+    for j, n in enumerate(old):
+        ks = torch.cat([hist_k[j], k[P + j:P + j + 1]]).float()
+        vs = torch.cat([hist_v[j], v[P + j:P + j + 1]]).float()
+        for h in range(Hq):
+            sc = ks[:, h // G] @ q[P + j, h].float() / math.sqrt(d)
+            o = torch.softmax(sc, 0) @ vs[:, h // G]
+            assert (out[P + j, h].float() - o).abs().max().item() <= 2e-2

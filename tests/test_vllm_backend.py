@@ -154,3 +154,102 @@ def test_paged_decode_attention_matches_explicit_attention():
                 s = ks[:pos + 1, h // 2] @ q[r, h].double() * scale
                 want = torch.softmax(s, 0) @ vs[:pos + 1, h // 2]
                 assert torch.allclose(out[r, h].double(), want, atol=1e-5)
+
+
+# --------------------------------------------------------------------------
+# v0 engine forward (patches/patch_loader_vllm_0_10_0.py:78-376)
+# --------------------------------------------------------------------------
+
+def _meta_v0(n_pre, n_dec, *, prefill=None, decode=None, **kw):
+    m = SimpleNamespace(num_prefill_tokens=n_pre, num_decode_tokens=n_dec,
+                        slot_mapping=torch.arange(n_pre + n_dec).view(-1, 1),
+                        prefill_metadata=prefill, decode_metadata=decode)
+    m.__dict__.update(kw)
+    return m
+
+
+def _prefill_meta(cu, tables=None):
+    cu_t = torch.tensor(cu, dtype=torch.int32)
+    lens = [cu[b + 1] - cu[b] for b in range(len(cu) - 1)]
+    return SimpleNamespace(seq_start_loc=cu_t, max_prefill_seq_len=max(lens),
+                           query_start_loc=cu_t, seq_lens_tensor=torch.tensor(lens),
+                           block_tables=tables)
+
+
+def _decode_meta(seq_lens, max_q=1, cu=None):
+    return SimpleNamespace(seq_lens_tensor=torch.tensor(seq_lens), max_decode_query_len=max_q,
+                           query_start_loc=None if cu is None else torch.tensor(cu),
+                           block_tables=torch.zeros(len(seq_lens), 4, dtype=torch.int32))
+
+
+def test_v0_mixed_batch_prefill_then_decode_rows():
+    # 7 + 3 prefill tokens (no block tables: the step's own rows), then 2
+    # decode tokens with one query each; the write uses the flattened mapping
+    calls, ops = _recording_ops()
+    fwd = vb.make_forward_v0(vb.ATTENTION_CONFIGS["flashprefill_llama"], ops)
+    q, k, v, kv, out = _tensors(T=12)
+    pm, dm = _prefill_meta([0, 7, 10]), _decode_meta([30, 12])
+    meta = _meta_v0(10, 2, prefill=pm, decode=dm)
+    assert fwd(FakeImpl(scale=0.2), None, q, k, v, kv, meta, output=out) is out
+    assert [c[0] for c in calls] == ["cache", "prefill", "decode"]
+    ck, cv, kc, vc, slots = calls[0][1]
+    assert ck is k and cv is v and slots.shape == (12,)
+    assert torch.equal(kc, kv[0]) and torch.equal(vc, kv[1])
+    a = calls[1][1]
+    assert [t.shape[0] for t in a[:4]] == [10, 10, 10, 10]
+    assert a[0].data_ptr() == q.data_ptr() and a[3].data_ptr() == out.data_ptr()
+    assert a[4] is pm.seq_start_loc and a[5] == 7 and a[6:] == (0.18, 128, 2, 4, 2)
+    d = calls[2][1]
+    assert d[0].shape[0] == 2 and d[0].data_ptr() == q[10].data_ptr()
+    assert d[3].data_ptr() == out[10].data_ptr()
+    assert d[4].tolist() == [0, 1, 2] and d[5] is dm.seq_lens_tensor
+    assert d[6] is dm.block_tables and d[7] == 0.2
+
+
+def test_v0_prefix_cached_prefill_and_varlen_decode_use_the_paged_cache():
+    calls, ops = _recording_ops()
+    fwd = vb.make_forward_v0(vb.ATTENTION_CONFIGS["flashprefill_qwen2"], ops)
+    q, k, v, kv, out = _tensors(T=9)
+    tables = torch.ones(2, 4, dtype=torch.int32)
+    pm = _prefill_meta([0, 4, 6], tables=tables)
+    dm = _decode_meta([20, 8], max_q=2, cu=[0, 2, 3])
+    fwd(FakeImpl(), None, q, k, v, kv, _meta_v0(6, 3, prefill=pm, decode=dm), output=out)
+    assert [c[0] for c in calls] == ["cache", "decode", "decode"]
+    p = calls[1][1]
+    assert p[0].shape[0] == 6 and torch.equal(p[1], kv[0]) and p[4] is pm.query_start_loc
+    assert p[5] is pm.seq_lens_tensor and p[6] is tables
+    d = calls[2][1]
+    assert d[0].shape[0] == 3 and d[4] is dm.query_start_loc
+
+
+def test_v0_profiling_run_guards_and_delegation():
+    calls, ops = _recording_ops()
+    fwd = vb.make_forward_v0(vb.ATTENTION_CONFIGS["flashprefill_qwen2"], ops)
+    q, k, v, kv, out = _tensors()
+    # an unallocated cache (profiling run): no write, prefill on the step's rows
+    fwd(FakeImpl(), None, q, k, v, torch.empty(0), _meta_v0(10, 0, prefill=_prefill_meta([0, 10])),
+        output=out)
+    assert [c[0] for c in calls] == ["prefill"]
+    calls.clear()
+    # encoder-decoder layers are delegated whole, their cache write included
+    enc_dec = FakeImpl(attn_type="encoder_decoder")
+    assert fwd(enc_dec, None, q, k, v, kv, _meta_v0(10, 0), output=out) == "enc"
+    assert [c[0] for c in calls] == ["encoder"]
+    with pytest.raises(ValueError):
+        fwd(FakeImpl(), None, q, k, v, kv, _meta_v0(10, 0), output=None)
+    with pytest.raises(NotImplementedError):
+        fwd(FakeImpl(), None, q, k, v, kv, _meta_v0(10, 0), output=out,
+            output_scale=torch.ones(1))
+    with pytest.raises(NotImplementedError):
+        fwd(FakeImpl(kv_cache_dtype="fp8"), None, q, k, v, kv, _meta_v0(10, 0), output=out)
+    plain = vb.make_forward_v0(vb.ATTENTION_CONFIGS["flashprefill_qwen2"])
+    with pytest.raises(NotImplementedError):
+        plain(FakeImpl(attn_type="encoder"), None, q, k, v, kv, _meta_v0(10, 0), output=out)
+
+
+def test_apply_patch_v0_replaces_forward():
+    class Impl(FakeImpl):
+        pass
+    _, ops = _recording_ops()
+    orig = vb.apply_patch_v0(Impl, "flashprefill_qwen3moe", ops)
+    assert orig is FakeImpl.forward and Impl.forward is not FakeImpl.forward
