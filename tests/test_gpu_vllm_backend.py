@@ -2,7 +2,9 @@
 (fp_kv_cache_write) against an index-copy reference, and a prefill step then
 a decode step through the hooked forward (stand-in impl and metadata; the
 prefill output equals a direct flash_prefill_varlen_func call bit for bit,
-the decode output matches explicit fp32 attention over the cached keys)."""
+the decode output matches explicit fp32 attention over the cached keys), and
+one mixed v0-engine step (prefill rows, then decode rows) through the v0
+forward."""
 
 import math
 from types import SimpleNamespace
