@@ -355,15 +355,15 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
     e = fp::launch_attn_f32(a, p->head_dim, p->block_size, a.total_slots, s);
   } else {
     // Persistent grid (every resident workgroup loops over its XCD's queue)
-    // once there are at least 8 slots per resident workgroup: it saves the
+    // once there are at least 4 slots per resident workgroup: it saves the
     // dispatcher's gap between a finished row and the next workgroup
-    // (128K attention -3 to -4.5 %, 16K -1.7 %). Below that, one workgroup
-    // per slot (the persistent loop's per-slot claim costs more than it saves
-    // on short rows: 4K +6 %, 8K +4 %).
+    // (128K attention -3 to -4.5 %, 16K -1.7 %, 8K call -1.4 %). Below that,
+    // one workgroup per slot (4K, 2.5 slots per workgroup: the persistent
+    // loop's per-slot claim costs more than it saves, +3 %).
     int64_t resident = 0;
     const int rc = resident_attn_workgroups(p->block_size, &resident);
     if (rc != FP_OK) return rc;
-    const bool persist = a.total_slots >= 8 * resident;
+    const bool persist = a.total_slots >= 4 * resident;
     const int64_t grid = persist ? resident : a.total_slots;
     e = fp::launch_attn(a, p->dtype, p->head_dim, p->block_size, grid, persist, s);
   }

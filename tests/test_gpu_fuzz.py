@@ -115,7 +115,8 @@ def test_random_large_configuration_persistent_attention(seed):
     per_cu = 2 if block == 128 else 4
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     # grow the longest sequence until Hq * (capacity of the block table) reaches
-    # 8 slots per resident workgroup, the host's threshold for the persistent grid
+    # 8 slots per resident workgroup, twice the host's threshold (4) for the
+    # persistent grid, so that every workgroup claims several slots
     while True:
         nb_max = (max(lens) + block - 1) // block
         cap = min(len(lens) * nb_max, (sum(lens) + (block - 1) * len(lens)) // block)
