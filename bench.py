@@ -410,7 +410,7 @@ def median(xs):
 
 
 def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines, dense_reps=3,
-            rounds=1):
+            rounds=1, min_region_ms=0.0):
     """Time one operator configuration (HIP events on the launch stream):
     the public entry point flash_prefill_varlen_func (its cached workspace
     and argument handling included: what a caller pays per call), the same
@@ -421,7 +421,10 @@ def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines, dense_
     public and prebuilt calls are timed alternately that many times (``steps``
     calls each) and the medians are reported: short configurations otherwise
     carry the first timed region's ramp-up (their first round runs up to
-    ~10 % slower)."""
+    ~10 % slower). With ``min_region_ms`` the number of calls per timed
+    region is raised until the region lasts about that long (a 4K call is
+    ~0.1 ms: five calls make a 0.5 ms region, where launch jitter and the
+    clock's ramp weigh in); the count used is reported as ``steps``."""
     import torch
     from flashprefill_amd import flash_prefill_varlen_func
     from flashprefill_amd.runtime import FlashPrefillCall
@@ -439,6 +442,9 @@ def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines, dense_
         public_call()
         call.run()
     torch.cuda.synchronize()
+    if min_region_ms > 0:
+        est = timed(call.run, 3)
+        steps = max(steps, min(400, math.ceil(min_region_ms / max(est, 1e-3))))
     print("bench: timing", file=sys.stderr, flush=True)
     pub_ms, pre_ms = [], []
     for _ in range(rounds):
@@ -482,6 +488,7 @@ def measure(q, k, v, cu, seq_lens, alpha, steps, warmup, dense_baselines, dense_
     exec_tflops = 4.0 * 128 * 128 * d * n_exec / (ms_attn * 1e-3) / 1e12
     dense_flops = sum(dense_causal_flops(s, Hq, d) for s in seq_lens)
     out = {
+        "steps": steps, "rounds": rounds,
         "ms_total": ms_total, "ms_total_prebuilt_call": ms_prebuilt,
         "ms_search": ms_search, "ms_attn": ms_attn,
         "ms_pool": ms_pool, "ms_score": ms_score, "ms_plan": ms_plan,
@@ -645,7 +652,8 @@ def config_results(config, steps, warmup, dense):
     for spec, alpha, name in config_cases(config):
         print(f"bench: config {config} {name}", file=sys.stderr, flush=True)
         q, k, v, cu = synth.make_inputs(spec, device=dev)
-        r = measure(q, k, v, cu, list(spec.seq_lens), alpha, steps, warmup, dense, rounds=3)
+        r = measure(q, k, v, cu, list(spec.seq_lens), alpha, steps, warmup, dense, rounds=3,
+                    min_region_ms=20.0)
         r.update({"case": name, "seq_lens": list(spec.seq_lens), "num_q_heads": spec.num_q_heads,
                   "num_kv_heads": spec.num_kv_heads, "head_dim": spec.head_dim, "alpha": alpha,
                   "seed": spec.seed})
