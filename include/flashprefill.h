@@ -117,7 +117,9 @@ typedef struct fp_ws_layout {
                             second list entry, diagonal block kept */
     size_t idx_off;
     size_t units_off;    /* split rows (16-bit inputs): int32 count at +0, then from +64
-                            records of 48 bytes: the row's item record, chunk, chunks */
+                            records of 48 bytes: the row's item record, chunk, chunks;
+                            then int32 arrival counters [Hq][unit_cap] (zeroed by the
+                            plan; the last chunk of a row to finish merges the row) */
     size_t part_off;     /* fp32 partial results of the chunks, per (head, unit):
                             acc[block][head_dim], m[block], l[block] */
     int64_t nb_sum_cap;  /* >= sum_b NB_b */
