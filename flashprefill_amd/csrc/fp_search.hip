@@ -52,6 +52,17 @@ __device__ __forceinline__ float block_max_lds(float x, float* red) {
   return r;
 }
 
+// max over lanes l and l ^ 32, in every lane (pair32_max without the operand
+// canonicalisation the compiler adds to fmaxf of exchanged bits; for the
+// non-NaN scores of the search this is the same value)
+__device__ __forceinline__ float pair32_max_raw(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
+                                                  __builtin_bit_cast(unsigned, x), false, false);
+  float y;
+  asm("v_max_f32 %0, %1, %2" : "=v"(y) : "v"(static_cast<unsigned>(r[0])), "v"(static_cast<unsigned>(r[1])));
+  return y;
+}
+
 // LDS scratch of select_row: block-reduction slots and the radix histogram
 constexpr int kSelectScratch = 104 + 256 * 4;
 
@@ -130,7 +141,9 @@ __device__ __forceinline__ void select_row(float* pl, float* ml, int n, int i, i
   int* pick = reinterpret_cast<int*>(static_cast<char*>(scratch) + 80);
   int* head3 = reinterpret_cast<int*>(static_cast<char*>(scratch) + 88);  // row record: j0, j1, diag
   uint32_t* hist = reinterpret_cast<uint32_t*>(static_cast<char*>(scratch) + 104);
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  // the wave index through readfirstlane: the compiler then knows it is
+  // wave-uniform, so loops and branches on it are scalar
+  const int t = threadIdx.x, lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6);
   if (t < 3) head3[t] = 0;
 
   float lm = -INFINITY;
@@ -239,7 +252,9 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
   int slot, h;
   map_item(blockIdx.x, a.Hq, slot, h);
   const int64_t nitems = sld(a.tab.seq_tile + a.B);
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  // the wave index through readfirstlane: the compiler then knows it is
+  // wave-uniform, so loops and branches on it are scalar
+  const int t = threadIdx.x, lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6);
   // The workgroup's rows: item `slot`, and with pair_rows also the item at the
   // other end of the heaviest-first order, so that every pair holds about the
   // same work (scored second, its query block loads during the first row's
@@ -308,11 +323,16 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
     // l32, dims 16 s + 8 half .. +7; columns past the row's last key read key
     // n - 1: their scores are computed and never stored)
     typename T::vec8 kb[KS];
+    // lane part of a key-operand address: chunk row of the half-wave, key l32
+    const uint32_t koff = half_off + 16u * static_cast<uint32_t>(l32);
     auto load_kb = [&](const Row& r, int tile) {
-      int ln = lane;
-      asm volatile("" : "+v"(ln));
-      const int j = min(32 * tile + (ln & 31), r.n - 1);
-      const uint32_t off = half_off + static_cast<uint32_t>(j) * 16u;
+      // a tile inside the row adds its scalar offset; the row's last tile
+      // clamps its keys to n - 1
+      uint32_t off = koff + 512u * static_cast<uint32_t>(tile);
+      if (32 * tile + 32 > r.n) {
+        asm volatile("" : "+v"(off));  // keep the clamp on the last tile's branch
+        off = half_off + 16u * static_cast<uint32_t>(min(32 * tile + l32, r.n - 1));
+      }
 #pragma unroll
       for (int s = 0; s < KS; ++s)
         kb[s] = as_vec8<T>(*reinterpret_cast<const uint4*>(r.kb0 + s * kb_step + off));
@@ -370,11 +390,24 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
 #pragma unroll
           for (int v = 0; v < 16; ++v) mx = fmaxf(mx, acc[rg][v]);
         if (tile + 1 < ntiles) {  // every column j < i: all BLK rows count
-          m = pair32_max(mx) * c;
+          m = pair32_max_raw(mx) * c;
 #pragma unroll
           for (int rg = 0; rg < RG; ++rg)
 #pragma unroll
             for (int v = 0; v < 16; ++v) sum += __builtin_amdgcn_exp2f(fmaf(acc[rg][v], c, -m));
+          sum = pair32_sum(sum);
+          // every column of a tile before the last is a key of the row
+          if (half == 0) {
+            pl[j] = sum;
+            ml[j] = m;
+            if (a.dump_p) {
+              float* dp = a.dump_p + (r.row_tri + 32 * tile);
+              float* dm = a.dump_m + (r.row_tri + 32 * tile);
+              dp[l32] = sum;
+              dm[l32] = m;
+            }
+          }
+          continue;
         } else {
           // last tile: j < i all rows, j == i the last row BLK - 1 only
           // (acc[RG - 1][15] of the upper half-wave), j > i none. The case is
@@ -458,7 +491,9 @@ __global__ __launch_bounds__(256, 2) void k_search_f32(SearchArgs a) {
   const int64_t t0 = rec.t0;
   const int n = i + 1;
   const int64_t row_tri = static_cast<int64_t>(h) * a.tri_cap + rec.tri;
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  // the wave index through readfirstlane: the compiler then knows it is
+  // wave-uniform, so loops and branches on it are scalar
+  const int t = threadIdx.x, lane = t & 63, w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int half = lane >> 5, l32 = lane & 31;
   const int kvh = h / (a.Hq / a.Hkv);
   const float c = a.sm_scale_log2;
