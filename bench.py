@@ -45,6 +45,10 @@ def parse():
     ap.add_argument("--alpha", type=float, default=0.18)
     ap.add_argument("--no-dense", action="store_true", help="skip the dense baselines")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--no-clock", action="store_true",
+                    help="skip the shader-clock / socket-power sampling (amd-smi child "
+                         "processes); for runs under rocprofv3, whose preloaded library would "
+                         "start the GPU in every child process")
     ap.add_argument("--no-configs", action="store_true",
                     help="leave out the configs 1, 2, 4 and 5 sub-reports of the bench line")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
@@ -784,20 +788,22 @@ def main():
     # shader clock and socket power while the attention, then the search,
     # runs back to back: both stages run below the 2.4 GHz clock ceiling,
     # held there by the card's power limit
-    print("bench: clock under load", file=sys.stderr, flush=True)
-    from flashprefill_amd.runtime import FlashPrefillCall
-    ccall = FlashPrefillCall(q, k, v, torch.empty_like(q), cu, S, alpha=args.alpha)
-    ccall.plan(); ccall.pool(); ccall.search(); ccall.attn()
+    clock = None
+    if not args.no_clock:
+        print("bench: clock under load", file=sys.stderr, flush=True)
+        from flashprefill_amd.runtime import FlashPrefillCall
+        ccall = FlashPrefillCall(q, k, v, torch.empty_like(q), cu, S, alpha=args.alpha)
+        ccall.plan(); ccall.pool(); ccall.search(); ccall.attn()
 
-    def search_only():
-        ccall.pool()
-        ccall.search()
-    clock = {"attention": clock_under_load(ccall.attn, 2.0),
-             "search": clock_under_load(search_only, 2.0),
-             "max_gfx_mhz": MAX_GFX_MHZ,
-             "method": "amd-smi metric -c (mean of the 8 XCDs' gfx clocks) and -p every 0.2 s "
-                       "while the stage runs back to back for 2 s; medians"}
-    del ccall
+        def search_only():
+            ccall.pool()
+            ccall.search()
+        clock = {"attention": clock_under_load(ccall.attn, 2.0),
+                 "search": clock_under_load(search_only, 2.0),
+                 "max_gfx_mhz": MAX_GFX_MHZ,
+                 "method": "amd-smi metric -c (mean of the 8 XCDs' gfx clocks) and -p every 0.2 s "
+                           "while the stage runs back to back for 2 s; medians"}
+        del ccall
 
     cpu = None
     if not args.no_cpu:
@@ -896,7 +902,7 @@ def main():
         "clock": clock,
         "cpu_baseline": cpu,
     }
-    if clock["attention"]:
+    if clock and clock["attention"]:
         # the same achieved rate against the peak scaled to the clock the
         # attention holds under the power limit (the nominal frac above stays
         # the reported one)
