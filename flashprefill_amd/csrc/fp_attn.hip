@@ -389,8 +389,13 @@ __device__ __forceinline__ bool attn_slot(const Args& a, int slot, int t, Tail t
     // those (and any item >= nitems) return below, so the loads are clamped
     const int64_t it = min(static_cast<int64_t>(item), a.nb_sum_cap - 1);
     rec = sld(a.tab.items + it);
-    const int4 rrec = sld(reinterpret_cast<const int4*>(a.rowrec) +
-                          static_cast<int64_t>(h) * a.nb_sum_cap + it);
+    int4 rrec = sld(reinterpret_cast<const int4*>(a.rowrec) +
+                    static_cast<int64_t>(h) * a.nb_sum_cap + it);
+    // block_size 256: the selection wrote the records of a row pair by tile
+    // (a second, dependent load; at ratio 1 the first load is independent)
+    if (a.ratio > 1)
+      rrec = sld(reinterpret_cast<const int4*>(a.rowrec) + static_cast<int64_t>(h) * a.nb_sum_cap +
+                 min(max(rec.tile, 0), static_cast<int32_t>(a.nb_sum_cap - 1)));
     if (item >= nitems) return false;
     // the chunks of a split row produce its output
     if (row_is_split(rec.i, (rec.L + BLK - 1) / BLK, a.last_n, a.split_blocks)) return false;

@@ -40,6 +40,14 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 int64_t elem_bytes(int dtype) { return dtype == FP_DTYPE_F32 ? 4 : 2; }
 
+// Block size of the plan, the work items, the index lists and the attention:
+// block_size itself for 64 and 128; for 256, selection blocks of 256 tokens
+// (pooling, scoring, selection) over a 128-token plan, the selection writing
+// each 256-row's list as the lists of its two 128-token rows (ratio 2), so
+// that the attention walks 128-key tiles as the reference's kernels do.
+int plan_block(const fp_problem* p) { return p->block_size == 256 ? 128 : p->block_size; }
+int block_ratio(const fp_problem* p) { return p->block_size / plan_block(p); }
+
 int validate(const fp_problem* p) {
   if (!p) return fail(FP_E_INVALID_ARG, "problem descriptor is NULL");
   if (!p->q || !p->k || !p->v || !p->o) return fail(FP_E_INVALID_ARG, "q/k/v/o must be non-NULL");
@@ -47,16 +55,26 @@ int validate(const fp_problem* p) {
     return fail(FP_E_UNSUPPORTED, "dtype %d unsupported (bf16, fp16 or fp32)", p->dtype);
   if (p->head_dim != 64 && p->head_dim != 128)
     return fail(FP_E_UNSUPPORTED, "head_dim %d unsupported (64 or 128)", p->head_dim);
-  if (p->block_size != 64 && p->block_size != 128)
-    return fail(FP_E_UNSUPPORTED, "block_size %d unsupported (64 or 128)", p->block_size);
+  if (p->block_size != 64 && p->block_size != 128 && p->block_size != 256)
+    return fail(FP_E_UNSUPPORTED, "block_size %d unsupported (64, 128 or 256)", p->block_size);
   if (p->num_q_heads < 1 || p->num_kv_heads < 1 || p->num_q_heads % p->num_kv_heads)
     return fail(FP_E_INVALID_ARG, "num_q_heads (%d) must be a positive multiple of num_kv_heads (%d)",
                 p->num_q_heads, p->num_kv_heads);
   if (p->batch < 1 || p->batch > fp::kMaxBatch)
     return fail(FP_E_INVALID_ARG, "batch %d outside [1, %d]", p->batch, fp::kMaxBatch);
-  if (p->max_seq_len < 1 || p->max_seq_len > fp::kMaxBlocks * p->block_size)
+  if (p->max_seq_len < 1 || p->max_seq_len > fp::kMaxBlocks * plan_block(p))
     return fail(FP_E_INVALID_ARG, "max_seq_len %d outside [1, %d] (%d blocks of %d tokens)",
-                p->max_seq_len, fp::kMaxBlocks * p->block_size, fp::kMaxBlocks, p->block_size);
+                p->max_seq_len, fp::kMaxBlocks * plan_block(p), fp::kMaxBlocks, plan_block(p));
+  if (p->dtype == FP_DTYPE_F32 && p->block_size == 256) {
+    // the fp32 search holds the 256-row query block (rows padded by 16 bytes)
+    // and a row's fp32 (p, m) in LDS
+    const int64_t nb = (p->max_seq_len + 127) / 128;
+    const int64_t lds = 256 * (static_cast<int64_t>(p->head_dim) + 4) * 4 + 8 * nb;
+    if (lds > 160 * 1024)
+      return fail(FP_E_UNSUPPORTED, "fp32 inputs at block_size 256 support up to %lld tokens at "
+                  "head_dim %d", static_cast<long long>((160 * 1024 - 256 * (p->head_dim + 4) * 4) / 8 * 128),
+                  p->head_dim);
+  }
   if (p->total_tokens < 0) return fail(FP_E_INVALID_ARG, "total_tokens < 0");
   if (!p->cu_seqlens) {
     if (p->uniform_seq_len < 0 || p->uniform_seq_len > p->max_seq_len)
@@ -87,7 +105,7 @@ int layout(const fp_problem* p, fp_ws_layout* L) {
   if (rc != FP_OK) return rc;
   memset(L, 0, sizeof(*L));
   const int64_t B = p->batch;
-  const int64_t blk = p->block_size;
+  const int64_t blk = plan_block(p);
   const int64_t nb_max = (p->max_seq_len + blk - 1) / blk;
   int64_t cap = (p->total_tokens + (blk - 1) * B) / blk;
   if (cap > B * nb_max) cap = B * nb_max;
@@ -218,7 +236,7 @@ fp::PlanArgs plan_args(const fp_problem* p, const fp_ws_layout& L, void* ws) {
   a.nb_max = L.nb_max;
   a.total_tokens = p->total_tokens;
   a.nb_sum_cap = L.nb_sum_cap;
-  a.block = p->block_size;
+  a.block = plan_block(p);
   a.last_n = p->last_n_block;
   a.split_blocks = L.split_blocks;
   a.units = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + L.units_off);
@@ -243,7 +261,8 @@ fp::PoolArgs pool_args(const fp_problem* p, const fp_ws_layout& L, void* ws) {
   a.nb_sum_cap = L.nb_sum_cap;
   a.B = p->batch;
   a.Hkv = p->num_kv_heads;
-  a.block = p->block_size;
+  a.block = plan_block(p);
+  a.ratio = block_ratio(p);
   return a;
 }
 
@@ -350,9 +369,11 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   // attention.
   a.arrivals = arrival_counters(p, L, ws);
   a.merge_inline = p->num_q_heads % 8 == 0 ? 1 : 0;
+  a.ratio = block_ratio(p);
+  const int blk = plan_block(p);
   hipError_t e;
   if (p->dtype == FP_DTYPE_F32) {
-    e = fp::launch_attn_f32(a, p->head_dim, p->block_size, a.total_slots, s);
+    e = fp::launch_attn_f32(a, p->head_dim, blk, a.total_slots, s);
   } else {
     // Persistent grid (every resident workgroup loops over its XCD's queue)
     // once there are at least 4 slots per resident workgroup: it saves the
@@ -361,14 +382,14 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
     // one workgroup per slot (4K, 2.5 slots per workgroup: the persistent
     // loop's per-slot claim costs more than it saves, +3 %).
     int64_t resident = 0;
-    const int rc = resident_attn_workgroups(p->block_size, &resident);
+    const int rc = resident_attn_workgroups(blk, &resident);
     if (rc != FP_OK) return rc;
     const bool persist = a.total_slots >= 4 * resident;
     const int64_t grid = persist ? resident : a.total_slots;
-    e = fp::launch_attn(a, p->dtype, p->head_dim, p->block_size, grid, persist, s);
+    e = fp::launch_attn(a, p->dtype, p->head_dim, blk, grid, persist, s);
   }
   if (e == hipSuccess && L.split_blocks > 0 && !a.merge_inline)
-    e = fp::launch_merge(a, p->dtype, p->head_dim, p->block_size, s);
+    e = fp::launch_merge(a, p->dtype, p->head_dim, blk, s);
   return e == hipSuccess ? FP_OK : hip_fail(e, "attention launch");
 }
 

@@ -33,7 +33,8 @@ struct PoolArgs {
   int64_t nb_sum_cap;
   int32_t B;
   int32_t Hkv;
-  int32_t block;  // tokens per block
+  int32_t block;  // tokens per block of the plan and the attention
+  int32_t ratio;  // selection blocks are ratio x block tokens (2 at block_size 256, else 1)
 };
 
 struct SearchArgs {
@@ -43,7 +44,8 @@ struct SearchArgs {
   const uint16_t* mk;
   int32_t* idx;
   int32_t* cnt;
-  int32_t* rowrec;    // per (head, item): {count, first entry, second entry, diagonal kept}
+  int32_t* rowrec;    // per (head, item), or per (head, tile) at block_size 256:
+                      // {count, first entry, second entry, diagonal kept}
   int64_t tri_cap;
   int64_t nb_sum_cap;
   const float* in_p;  // select-only mode: caller's block scores
@@ -55,6 +57,11 @@ struct SearchArgs {
   float alpha;
   int32_t sink, window, last_n, native, min_budget;
   int32_t pair_rows;  // 16-bit score kernel: two rows per workgroup (set by launch_search)
+  // (Selection blocks of 256 tokens over the 128-token plan, block_size 256:
+  // the workgroup of item (b, 2i) scores and selects 256-row i and writes the
+  // 128-granularity lists of rows 2i and 2i + 1, those of item (b, 2i + 1)
+  // return at once; pooled key block j sits at slot 2j. The search kernels'
+  // block template of 256 selects this.)
 };
 
 struct AttnArgs {
@@ -66,7 +73,8 @@ struct AttnArgs {
   int64_t qst, qhs, kst, khs, vst, vhs, ost, ohs;
   const int32_t* idx;
   const int32_t* cnt;
-  const int32_t* rowrec;  // per (head, item): {count, first entry, second entry, diagonal kept}
+  const int32_t* rowrec;  // per (head, item), or per (head, tile) when ratio > 1:
+                          // {count, first entry, second entry, diagonal kept}
   int64_t tri_cap;
   int64_t nb_sum_cap;
   int32_t B, Hq, Hkv;
@@ -90,6 +98,7 @@ struct AttnArgs {
   // otherwise k_merge does
   int32_t* arrivals;
   int32_t merge_inline;
+  int32_t ratio;  // > 1: row records are indexed by tile (block_size 256)
 };
 
 struct KvCacheArgs {

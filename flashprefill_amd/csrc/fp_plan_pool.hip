@@ -296,9 +296,12 @@ __global__ __launch_bounds__(256) void k_pool(PoolArgs a) {
   if (g >= nsum) return;
   const int b = find_seq(a.tab.seq_tile, a.B, g);
   const int i = static_cast<int>(g - a.tab.seq_tile[b]);
+  // a selection block of ratio plan blocks is pooled by the workgroup of its
+  // first plan block, into that block's slot
+  if (i % a.ratio) return;
   const int L = a.tab.seq_len[b];
   pool_block<T, D>(a, g, hh, a.tab.seq_start[b] + static_cast<int64_t>(i) * a.block,
-                   min(a.block, L - i * a.block));
+                   min(a.block * a.ratio, L - i * a.block));
 }
 
 // ---------------------------------------------------------------------------
@@ -481,8 +484,9 @@ __global__ __launch_bounds__(256) void k_plan_pool(PlanArgs pa, PoolArgs a) {
   int b = 0;
   while (b + 1 < a.B && sp.tile[b + 1] <= g) ++b;
   const int i = static_cast<int>(g - sp.tile[b]);
+  if (i % a.ratio) return;
   pool_block<T, D>(a, g, hh, sp.start[b] + static_cast<int64_t>(i) * a.block,
-                   min(a.block, sp.len[b] - i * a.block));
+                   min(a.block * a.ratio, sp.len[b] - i * a.block));
 }
 
 // fp32 keys: the block mean summed in fp64 (in row order) and rounded once to
@@ -494,9 +498,10 @@ __global__ __launch_bounds__(256) void k_pool_f32(PoolArgs a, int head_dim) {
   if (g >= nsum) return;
   const int b = find_seq(a.tab.seq_tile, a.B, g);
   const int i = static_cast<int>(g - a.tab.seq_tile[b]);
+  if (i % a.ratio) return;
   const int L = a.tab.seq_len[b];
   const int64_t t0 = a.tab.seq_start[b] + static_cast<int64_t>(i) * a.block;
-  const int rows = min(a.block, L - i * a.block);
+  const int rows = min(a.block * a.ratio, L - i * a.block);
   const float* k = reinterpret_cast<const float*>(a.k);
   // chunk-major: dims 4c .. 4c+3 of (g, hh) are entry g of chunk row hh * d / 4 + c
   float* out = reinterpret_cast<float*>(a.mk);

@@ -131,9 +131,19 @@ __device__ __forceinline__ uint32_t budget_threshold(const float* pl, int n, int
 // rounded and monotone, the max of the normalised scores is the normalised
 // max. The compaction loops use alternating count slots, one barrier per
 // 256 entries.
+//
+// At ratio 2 (block_size 256) the row is 256-row i of its sequence and the
+// outputs are the 128-granularity lists of plan rows 2i (list / count /
+// row_rec) and 2i + 1 (list_b / count_b / row_rec_b, null when the sequence
+// ends inside row 2i): a kept 256-block j < i is plan blocks 2j, 2j + 1 in
+// both, the kept diagonal j = i is block 2i in row 2i (its keys 256i + 128 ..
+// are all after the row's queries) and blocks 2i, 2i + 1 in row 2i + 1.
+template <int RATIO>
 __device__ __forceinline__ void select_row(float* pl, float* ml, int n, int i, int nb,
                                            const SearchArgs& a,
-                           int32_t* list, int32_t* count, int32_t* row_rec, void* scratch) {
+                           int32_t* list, int32_t* count, int32_t* row_rec, void* scratch,
+                           int32_t* list_b = nullptr, int32_t* count_b = nullptr,
+                           int32_t* row_rec_b = nullptr) {
 #pragma clang fp contract(off)
   float* redf = static_cast<float*>(scratch);
   double* redd = reinterpret_cast<double*>(static_cast<char*>(scratch) + 16);
@@ -212,7 +222,16 @@ __device__ __forceinline__ void select_row(float* pl, float* ml, int n, int i, i
     for (int k = 0; k < w; ++k) off += wtot[c2 + k];
     if (keep) {
       const int pos = off + lanes_below(bal);
-      list[pos] = j;
+      if constexpr (RATIO == 1) {
+        list[pos] = j;
+      } else {
+        list[2 * pos] = 2 * j;
+        if (j < i) list[2 * pos + 1] = 2 * j + 1;
+        if (list_b) {
+          list_b[2 * pos] = 2 * j;
+          list_b[2 * pos + 1] = 2 * j + 1;
+        }
+      }
       if (pos < 2) head3[pos] = j;
     }
     if (j == i) head3[2] = keep ? 1 : 0;
@@ -220,10 +239,21 @@ __device__ __forceinline__ void select_row(float* pl, float* ml, int n, int i, i
   }
   lds_barrier();  // head3 complete
   if (t == 0) {
-    *count = running;
     // the attention kernel's row record: one 16-byte load gives the count,
     // the first two entries and whether the diagonal block is kept
-    *reinterpret_cast<int4*>(row_rec) = make_int4(running, head3[0], head3[1], head3[2]);
+    if constexpr (RATIO == 1) {
+      *count = running;
+      *reinterpret_cast<int4*>(row_rec) = make_int4(running, head3[0], head3[1], head3[2]);
+    } else {
+      const int f0 = head3[0], dg = head3[2];
+      const int ca = 2 * running - dg;
+      *count = ca;
+      *reinterpret_cast<int4*>(row_rec) = make_int4(ca, 2 * f0, f0 < i ? 2 * f0 + 1 : 0, dg);
+      if (list_b) {
+        *count_b = 2 * running;
+        *reinterpret_cast<int4*>(row_rec_b) = make_int4(2 * running, 2 * f0, 2 * f0 + 1, dg);
+      }
+    }
   }
 }
 
@@ -239,11 +269,15 @@ __device__ __forceinline__ int qswz(int r) {
 template <int D, int BLK, bool FROM_SCORES>
 constexpr size_t search_q_bytes() { return FROM_SCORES ? kSelectScratch : BLK * D * 2; }
 
+// BLK is the selection block: 64 or 128 (the plan's block, ratio 1), or 256
+// over a 128-token plan (ratio 2).
 template <typename T, int D, int BLK, bool FROM_SCORES>
-__global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
+__global__ __launch_bounds__(256, BLK > 128 ? 2 : 4) void k_search(SearchArgs a) {
   // 4 workgroups per CU at BLK = 128: 4 x (32 KB query block + 2 x 4 KB p / m
-  // at 1024 blocks) = 160 KB of LDS, and at most 128 VGPRs per wave
+  // at 1024 blocks) = 160 KB of LDS, and at most 128 VGPRs per wave (BLK =
+  // 256: a 64 KB query block and 8 row groups of accumulators, two per CU)
   constexpr int RG = BLK / 32;  // 32-row groups of the query block
+  constexpr int RATIO = BLK > 128 ? 2 : 1;  // selection blocks per plan block
   extern __shared__ uint4 dyn4[];
   uint4* sq = dyn4;  // the query block (score mode only)
   float* pl = reinterpret_cast<float*>(reinterpret_cast<char*>(dyn4) +
@@ -268,19 +302,33 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
   } else if (item_a >= nitems) {
     return;
   }
+  // ratio 2: plan row 2i + 1 is selected together with row 2i
+  if constexpr (RATIO > 1)
+    if (sld(a.tab.items + item_a).i % RATIO) return;
   auto select = [&](const ItemRec& rec, int64_t item, int64_t row_tri, void* scratch) {
     int32_t* list = a.idx + row_tri;
     int32_t* count = a.cnt + static_cast<int64_t>(h) * a.nb_sum_cap + rec.tile;
-    int32_t* row_rec = a.rowrec + 4 * (static_cast<int64_t>(h) * a.nb_sum_cap + item);
     const int64_t tile_b = rec.tile - rec.i;
     const int nb = static_cast<int>(sld(a.tab.seq_tile + rec.b + 1) - tile_b);
-    select_row(pl, ml, rec.i + 1, rec.i, nb, a, list, count, row_rec, scratch);
+    if constexpr (RATIO == 1) {
+      int32_t* row_rec = a.rowrec + 4 * (static_cast<int64_t>(h) * a.nb_sum_cap + item);
+      select_row<1>(pl, ml, rec.i + 1, rec.i, nb, a, list, count, row_rec, scratch);
+    } else {
+      // 256-row i = rec.i / 2 writes plan rows rec.i and rec.i + 1 (when the
+      // sequence has it), records by tile
+      const int i = rec.i / RATIO;
+      int32_t* row_rec = a.rowrec + 4 * (static_cast<int64_t>(h) * a.nb_sum_cap + rec.tile);
+      const bool has_b = rec.i + 1 < nb;
+      select_row<RATIO>(pl, ml, i + 1, i, (nb + RATIO - 1) / RATIO, a, list, count, row_rec,
+                        scratch, has_b ? list + rec.i + 1 : nullptr, has_b ? count + 1 : nullptr,
+                        has_b ? row_rec + 4 : nullptr);
+    }
   };
 
   if constexpr (FROM_SCORES) {
     const ItemRec rec = sld(a.tab.items + item_a);
     const int64_t row_tri = static_cast<int64_t>(h) * a.tri_cap + rec.tri;
-    for (int j = t; j <= rec.i; j += 256) {
+    for (int j = t; j <= rec.i / RATIO; j += 256) {
       pl[j] = a.in_p[row_tri + j];
       ml[j] = a.in_m[row_tri + j];
     }
@@ -301,10 +349,12 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
     // bytes. kb0: chunk row 0 at the sequence's first key; k-step s reads
     // chunk row 2 s (the lower half-wave) and 2 s + 1 (the upper), kb_step
     // bytes apart per s; the lane part of an address is a 32-bit byte offset.
+    // Ratio 2: the row is 256-row i = rec.i / 2 and pooled key block j sits
+    // at slot 2j of the sequence's 128-token blocks.
     struct Row {
       ItemRec rec;
       int64_t row_tri;
-      int n, ntiles;
+      int i, n, ntiles;  // selection row, its keys, 32-key tiles
       const char* kb0;
     };
     const int64_t kb_step = 2 * a.nb_sum_cap * 16;
@@ -312,7 +362,8 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
       Row r;
       r.rec = sld(a.tab.items + item);
       r.row_tri = static_cast<int64_t>(h) * a.tri_cap + r.rec.tri;
-      r.n = r.rec.i + 1;
+      r.i = r.rec.i / RATIO;
+      r.n = r.i + 1;
       r.ntiles = (r.n + 31) >> 5;
       const int64_t tile_b = r.rec.tile - r.rec.i;
       r.kb0 = reinterpret_cast<const char*>(a.mk) +
@@ -324,14 +375,15 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
     // n - 1: their scores are computed and never stored)
     typename T::vec8 kb[KS];
     // lane part of a key-operand address: chunk row of the half-wave, key l32
-    const uint32_t koff = half_off + 16u * static_cast<uint32_t>(l32);
+    constexpr uint32_t kstride = 16u * RATIO;  // bytes per key
+    const uint32_t koff = half_off + kstride * static_cast<uint32_t>(l32);
     auto load_kb = [&](const Row& r, int tile) {
       // a tile inside the row adds its scalar offset; the row's last tile
       // clamps its keys to n - 1
-      uint32_t off = koff + 512u * static_cast<uint32_t>(tile);
+      uint32_t off = koff + 32u * kstride * static_cast<uint32_t>(tile);
       if (32 * tile + 32 > r.n) {
         asm volatile("" : "+v"(off));  // keep the clamp on the last tile's branch
-        off = half_off + 16u * static_cast<uint32_t>(min(32 * tile + l32, r.n - 1));
+        off = half_off + kstride * static_cast<uint32_t>(min(32 * tile + l32, r.n - 1));
       }
 #pragma unroll
       for (int s = 0; s < KS; ++s)
@@ -346,21 +398,21 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
       TileLanes<D, BLK, 4> tq;
       tq.init(a.qst, __builtin_amdgcn_readfirstlane(w), lane);
       issue_tile<D, BLK, 4>(sq, a.q + r.rec.t0 * a.qst + static_cast<int64_t>(h) * a.qhs, a.qst,
-                            tq, r.rec.i, r.rec.L, __builtin_amdgcn_readfirstlane(w), lane);
+                            tq, r.i, r.rec.L, __builtin_amdgcn_readfirstlane(w), lane);
     };
     auto first_kb = [&](const Row& r) {
       if (w < r.ntiles) load_kb(r, w);
     };
     auto land = [&](const Row& r) {
       asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-      if ((r.rec.i + 1) * BLK > r.rec.L) {
+      if ((r.i + 1) * BLK > r.rec.L) {
         for (int cidx = t; cidx < BLK * CH; cidx += 256)
-          if (r.rec.i * BLK + cidx / CH >= r.rec.L) sq[cidx] = zero4();
+          if (r.i * BLK + cidx / CH >= r.rec.L) sq[cidx] = zero4();
         __syncthreads();
       }
     };
     auto score = [&](const Row& r) {
-      const int n = r.n, ntiles = r.ntiles, i = r.rec.i;
+      const int n = r.n, ntiles = r.ntiles, i = r.i;
       for (int tile = w; tile < ntiles; tile += 4) {
         const int j = 32 * tile + l32;
         const bool jv = j < n;
@@ -477,6 +529,7 @@ __global__ __launch_bounds__(256, 4) void k_search(SearchArgs a) {
 template <int D, int BLK>
 __global__ __launch_bounds__(256, 2) void k_search_f32(SearchArgs a) {
   constexpr int RG = BLK / 32, QS = D + 4, KS = D / 2;
+  constexpr int RATIO = BLK > 128 ? 2 : 1;  // selection blocks per plan block
   extern __shared__ uint4 dyn4[];
   float* sq = reinterpret_cast<float*>(dyn4);  // BLK rows of QS floats
   float* pl = sq + BLK * QS;
@@ -486,8 +539,11 @@ __global__ __launch_bounds__(256, 2) void k_search_f32(SearchArgs a) {
   const int64_t nitems = sld(a.tab.seq_tile + a.B);
   if (item >= nitems) return;
   const ItemRec rec = sld(a.tab.items + item);
-  const int b = rec.b, i = rec.i, L = rec.L;
-  const int64_t tile_b = rec.tile - i;
+  // ratio 2: 256-row i = rec.i / 2 (plan row 2i + 1 is selected with row 2i),
+  // pooled key block j at slot 2j
+  if (rec.i % RATIO) return;
+  const int b = rec.b, i = rec.i / RATIO, L = rec.L;
+  const int64_t tile_b = rec.tile - rec.i;
   const int64_t t0 = rec.t0;
   const int n = i + 1;
   const int64_t row_tri = static_cast<int64_t>(h) * a.tri_cap + rec.tri;
@@ -519,7 +575,8 @@ __global__ __launch_bounds__(256, 2) void k_search_f32(SearchArgs a) {
     const bool jv = j < n;
     float kb[KS];
     // this lane's dims half * KS .. : chunks half * KS / 4 + s4
-    const float* kr = mk + (static_cast<int64_t>(half) * (KS / 4) * a.nb_sum_cap + (jv ? j : 0)) * 4;
+    const float* kr =
+        mk + (static_cast<int64_t>(half) * (KS / 4) * a.nb_sum_cap + (jv ? RATIO * j : 0)) * 4;
 #pragma unroll
     for (int s4 = 0; s4 < KS / 4; ++s4) {
       const float4 x = jv ? *reinterpret_cast<const float4*>(kr + s4 * a.nb_sum_cap * 4)
@@ -567,9 +624,17 @@ __global__ __launch_bounds__(256, 2) void k_search_f32(SearchArgs a) {
   __syncthreads();
   int32_t* list = a.idx + row_tri;
   int32_t* count = a.cnt + static_cast<int64_t>(h) * a.nb_sum_cap + rec.tile;
-  int32_t* row_rec = a.rowrec + 4 * (static_cast<int64_t>(h) * a.nb_sum_cap + item);
   const int nb = static_cast<int>(sld(a.tab.seq_tile + b + 1) - tile_b);
-  select_row(pl, ml, n, i, nb, a, list, count, row_rec, dyn4);
+  if constexpr (RATIO == 1) {
+    int32_t* row_rec = a.rowrec + 4 * (static_cast<int64_t>(h) * a.nb_sum_cap + item);
+    select_row<1>(pl, ml, n, i, nb, a, list, count, row_rec, dyn4);
+  } else {
+    int32_t* row_rec = a.rowrec + 4 * (static_cast<int64_t>(h) * a.nb_sum_cap + rec.tile);
+    const bool has_b = rec.i + 1 < nb;
+    select_row<RATIO>(pl, ml, n, i, (nb + RATIO - 1) / RATIO, a, list, count, row_rec, dyn4,
+                      has_b ? list + rec.i + 1 : nullptr, has_b ? count + 1 : nullptr,
+                      has_b ? row_rec + 4 : nullptr);
+  }
 }
 
 template <int D, int BLK>
@@ -601,14 +666,25 @@ hipError_t launch_search_t(const SearchArgs& a, int64_t grid, hipStream_t s) {
   return hipGetLastError();
 }
 
+// block: the selection block (64, 128 or 256)
 template <typename T, int D>
 hipError_t launch_search_d(const SearchArgs& a, int block, int64_t grid, bool from_scores,
                            hipStream_t s) {
+  if (block == 256)
+    return from_scores ? launch_search_t<T, D, 256, true>(a, grid, s)
+                       : launch_search_t<T, D, 256, false>(a, grid, s);
   if (block == 128)
     return from_scores ? launch_search_t<T, D, 128, true>(a, grid, s)
                        : launch_search_t<T, D, 128, false>(a, grid, s);
   return from_scores ? launch_search_t<T, D, 64, true>(a, grid, s)
                      : launch_search_t<T, D, 64, false>(a, grid, s);
+}
+
+template <int D>
+hipError_t launch_search_f32_d(const SearchArgs& a, int block, int64_t grid, hipStream_t s) {
+  if (block == 256) return launch_search_f32_t<D, 256>(a, grid, s);
+  return block == 128 ? launch_search_f32_t<D, 128>(a, grid, s)
+                      : launch_search_f32_t<D, 64>(a, grid, s);
 }
 
 // Problems of at least this many (head, row) items score two rows per
@@ -621,18 +697,15 @@ hipError_t launch_search(const SearchArgs& args, int dtype, int head_dim, int bl
   if (grid <= 0) return hipSuccess;
   SearchArgs a = args;
   a.pair_rows = 0;
-  if (dtype != FP_DTYPE_F32 && !from_scores && grid >= kPairRowsMin) {
+  if (dtype != FP_DTYPE_F32 && !from_scores && block != 256 && grid >= kPairRowsMin) {
     a.pair_rows = 1;
     grid = static_cast<int64_t>(a.Hq) * ((grid / a.Hq + 1) / 2);  // grid = Hq x item capacity
   }
   if (dtype == FP_DTYPE_F32) {
     if (from_scores)  // selection only: no input element is read
       return launch_search_d<BF16, 128>(a, block, grid, true, s);
-    if (head_dim == 128)
-      return block == 128 ? launch_search_f32_t<128, 128>(a, grid, s)
-                          : launch_search_f32_t<128, 64>(a, grid, s);
-    return block == 128 ? launch_search_f32_t<64, 128>(a, grid, s)
-                        : launch_search_f32_t<64, 64>(a, grid, s);
+    return head_dim == 128 ? launch_search_f32_d<128>(a, block, grid, s)
+                           : launch_search_f32_d<64>(a, block, grid, s);
   }
   if (dtype == FP_DTYPE_BF16)
     return head_dim == 128 ? launch_search_d<BF16, 128>(a, block, grid, from_scores, s)

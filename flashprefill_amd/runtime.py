@@ -102,6 +102,10 @@ class FlashPrefillCall:
         self.batch = int(batch)
         self.max_seq_len = int(max_seq_len)
         self.Hq, self.Hkv, self.d = Hq, Hkv, d
+        # block_size 256: 256-token selection blocks (pooled K, block scores)
+        # over a 128-token plan (work items, index lists, attention)
+        self.block = int(block_size)
+        self.ratio = 2 if self.block == 256 else 1
         P = _lib.FpProblem()
         P.q, P.k, P.v, P.o = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
         P.q_stride_tok, P.q_stride_head = q.stride(0), q.stride(1)
@@ -194,15 +198,32 @@ class FlashPrefillCall:
         tile, _, _, _ = self.seq_tables()
         return self._view(self.layout.items_off, torch.int32, 8 * tile[-1]).view(-1, 8)[:, :2]
 
+    def sel_tables(self) -> List[int]:
+        """Prefix sums of the selection blocks per sequence (the plan's block
+        counts, halved and rounded up at block_size 256)."""
+        tile, _, _, _ = self.seq_tables()
+        out = [0]
+        for b in range(self.batch):
+            nb = tile[b + 1] - tile[b]
+            out.append(out[-1] + (nb + self.ratio - 1) // self.ratio)
+        return out
+
     def pooled_k(self) -> torch.Tensor:
-        """Pooled K as (sum NB, Hkv, d); the workspace holds it chunk-major
-        (16-byte chunks of all key blocks of one (kv head, chunk) in a row)."""
+        """Pooled K as (sum NB, Hkv, d) over the selection blocks (sequence b
+        at rows sel_tables()[b] ..); the workspace holds it chunk-major
+        (16-byte chunks of all key blocks of one (kv head, chunk) in a row),
+        selection block j of a sequence at plan slot ratio * j."""
         tile, _, _, _ = self.seq_tables()
         cap, dt = self.layout.nb_sum_cap, self.tensors[0].dtype
         e = 16 // torch.tensor([], dtype=dt).element_size()
         raw = self._view(self.layout.mk_off, dt, self.Hkv * self.d * cap)
-        return (raw.view(self.Hkv, self.d // e, cap, e)[:, :, :tile[-1]]
-                .permute(2, 0, 1, 3).reshape(tile[-1], self.Hkv, self.d))
+        slots = (raw.view(self.Hkv, self.d // e, cap, e)[:, :, :tile[-1]]
+                 .permute(2, 0, 1, 3).reshape(tile[-1], self.Hkv, self.d))
+        if self.ratio == 1:
+            return slots
+        keep = [tile[b] + j for b in range(self.batch)
+                for j in range(0, tile[b + 1] - tile[b], self.ratio)]
+        return slots[torch.tensor(keep, dtype=torch.long, device=slots.device)]
 
     def counts(self) -> torch.Tensor:
         L = self.layout
@@ -259,30 +280,36 @@ class FlashPrefillCall:
                     return False
         return True
 
+    def _score_slots(self, b: int, tile, tri):
+        """Selection-granularity (row i, block j <= i) cells of sequence b
+        and their positions in the triangular layout: row i's scores sit in
+        the list slots of plan row ratio * i."""
+        nb = (tile[b + 1] - tile[b] + self.ratio - 1) // self.ratio
+        r, c = torch.tril_indices(nb, nb)
+        pr = self.ratio * r
+        return nb, r, c, tri[b] + pr * (pr + 1) // 2 + c
+
     def tri_scores(self, scores: Sequence[torch.Tensor]) -> torch.Tensor:
-        """Pack per-sequence (Hq, NB, NB) fp32 arrays into the triangular
-        (Hq * tri_cap) device layout that fp_select reads."""
+        """Pack per-sequence (Hq, NB, NB) fp32 arrays (selection blocks) into
+        the triangular (Hq * tri_cap) device layout that fp_select reads."""
         tile, tri, _, _ = self.seq_tables()
         L = self.layout
         out = torch.zeros(self.Hq, L.tri_cap, dtype=torch.float32)
         for b, s in enumerate(scores):
-            nb = tile[b + 1] - tile[b]
-            r, c = torch.tril_indices(nb, nb)
-            pos = tri[b] + r * (r + 1) // 2 + c
+            _, r, c, pos = self._score_slots(b, tile, tri)
             out[:, pos] = s[:, r, c].float()
         return out.reshape(-1).to(self.device)
 
     def untri_scores(self, flat: torch.Tensor) -> List[torch.Tensor]:
         """Inverse of tri_scores: device triangular dump -> per-sequence
-        (Hq, NB, NB) CPU arrays (upper triangle = NaN)."""
+        (Hq, NB, NB) CPU arrays over the selection blocks (upper triangle =
+        NaN)."""
         tile, tri, _, _ = self.seq_tables()
         L = self.layout
         flat = flat.view(self.Hq, L.tri_cap).cpu()
         out = []
         for b in range(self.batch):
-            nb = tile[b + 1] - tile[b]
-            r, c = torch.tril_indices(nb, nb)
-            pos = tri[b] + r * (r + 1) // 2 + c
+            nb, r, c, pos = self._score_slots(b, tile, tri)
             full = torch.full((self.Hq, nb, nb), float("nan"))
             full[:, r, c] = flat[:, pos]
             out.append(full)

@@ -43,7 +43,7 @@ extern "C" {
 
 #define FP_OK 0
 #define FP_E_INVALID_ARG (-1)   /* shapes, strides, alignment or scalars out of range */
-#define FP_E_UNSUPPORTED (-2)   /* valid for the reference but not built here (e.g. block 256) */
+#define FP_E_UNSUPPORTED (-2)   /* valid for the reference but not built here (e.g. head_dim 256) */
 #define FP_E_LAUNCH (-3)        /* a HIP launch or runtime call failed */
 
 #define FP_DTYPE_BF16 0
@@ -81,7 +81,8 @@ typedef struct fp_problem {
     int32_t num_kv_heads;
     int32_t head_dim;      /* 64 or 128 */
     int32_t dtype;         /* FP_DTYPE_BF16, FP_DTYPE_F16 or FP_DTYPE_F32 */
-    int32_t block_size;    /* 64 or 128 */
+    int32_t block_size;    /* 64, 128 or 256 (256: 256-token selection blocks over a
+                              128-token plan, lists and attention; see below) */
     /* selection */
     float alpha;
     int32_t attention_sink;
@@ -100,7 +101,14 @@ typedef struct fp_problem {
  *   p/m dumps  same triangular index with j in place of n           (fp32)
  * tile(b) = sum_{b'<b} NB_b', tri(b) = sum_{b'<b} NB_b'(NB_b'+1)/2, read back
  * from seq_tile / seq_tri (int64, batch+1 entries). Entries of skipped or
- * never-selected slots are not written (the workspace is not cleared). */
+ * never-selected slots are not written (the workspace is not cleared).
+ * NB_b, the items, counts and lists count blocks of the plan: block_size, or
+ * 128 tokens at block_size 256. There the selection works on 256-token
+ * blocks: pooled block j of sequence b sits at j' = 2j above, the scores
+ * (dumps and fp_select input) of 256-row i are in the list slots of plan row
+ * 2i (n = j), and each kept 256-block j is listed as plan blocks 2j, 2j + 1
+ * in rows 2i and 2i + 1 (row 2i omits 2i + 1 when j = i, whose keys follow
+ * all of its queries). */
 typedef struct fp_ws_layout {
     size_t total_bytes;
     size_t status_off;   /* uint32 status flags */
@@ -113,8 +121,9 @@ typedef struct fp_ws_layout {
                             int64 seq_start, seq_tri[b] + i (i + 1) / 2 */
     size_t mk_off;
     size_t cnt_off;
-    size_t rowrec_off;   /* int32[Hq * nb_sum_cap][4] by (head, item): count, first and
-                            second list entry, diagonal block kept */
+    size_t rowrec_off;   /* int32[Hq * nb_sum_cap][4] by (head, item), by (head, tile)
+                            at block_size 256: count, first and second list entry,
+                            diagonal block kept */
     size_t idx_off;
     size_t units_off;    /* split rows (16-bit inputs): int32 count at +0, then from +64
                             records of 48 bytes: the row's item record, chunk, chunks;
@@ -125,7 +134,7 @@ typedef struct fp_ws_layout {
     int64_t nb_sum_cap;  /* >= sum_b NB_b */
     int64_t tri_cap;     /* >= sum_b NB_b (NB_b + 1) / 2 */
     int64_t unit_cap;    /* >= number of chunk units (0: no row is split) */
-    int32_t nb_max;      /* ceil(max_seq_len / block_size) */
+    int32_t nb_max;      /* ceil(max_seq_len / plan block) */
     int32_t split_blocks; /* blocks per chunk of a split row (0: no row is split) */
 } fp_ws_layout;
 

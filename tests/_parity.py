@@ -164,6 +164,25 @@ def every_row_vs_closed_form(call, out: torch.Tensor, *, block: int = 128,
     return err_max, err_sum / max(n_el, 1), n_rows
 
 
+def expand_sel(sel: torch.Tensor, ratio: int, nb_plan: int) -> torch.Tensor:
+    """A (Hq, NB, NB) selection over selection blocks (256 tokens at ratio 2)
+    as the (Hq, nb_plan, nb_plan) lists over the plan's 128-token blocks must
+    hold it: plan block c of plan row r is listed iff selection block c // 2
+    is selected for selection row r // 2 and c <= r (the upper half of the
+    diagonal 256-block is after every query of the lower plan row)."""
+    if ratio == 1:
+        return sel
+    r = torch.arange(nb_plan)
+    blk = r // ratio
+    return sel[:, blk][:, :, blk] & (r.view(-1, 1) >= r.view(1, -1))
+
+
+def collapse_sel(sel_plan: torch.Tensor, ratio: int) -> torch.Tensor:
+    """The selection-block view of plan-granularity lists: (row 2i, block 2j)
+    stands for selection cell (i, j)."""
+    return sel_plan if ratio == 1 else sel_plan[:, ::ratio, ::ratio]
+
+
 def seq_slices(cu: Sequence[int]):
     return [(int(cu[b]), int(cu[b + 1])) for b in range(len(cu) - 1)]
 
@@ -187,6 +206,7 @@ def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n
                             window_size=window, last_n_block=last_n, native_normalize=native,
                             min_budget=min_budget, block_size=block)
     rep = StageReport(pool_exact=k.dtype != torch.float32)
+    ratio = call.ratio  # 2 at block 256: selection blocks of two plan blocks
     call.plan()
     call.pool()
     dump_p, dump_m = call.search(dump=True)
@@ -194,8 +214,14 @@ def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n
     assert call.status() == 0
     tile, tri, start, lens = call.seq_tables()
     assert lens == [b - a for a, b in seq_slices(cu_list)]
+    stile = call.sel_tables()
     mk_gpu = call.pooled_k().cpu()
-    gpu_sel = call.selection_masks()
+    plan_sel = call.selection_masks()
+    # the plan-granularity lists are exactly the expansion of the selection
+    gpu_sel = [collapse_sel(x, ratio) for x in plan_sel]
+    for b in range(len(plan_sel)):
+        assert torch.equal(expand_sel(gpu_sel[b], ratio, plan_sel[b].shape[-1]), plan_sel[b]), \
+            f"sequence {b}: plan lists are not the expansion of the selection"
     assert call.ordered_lists_ok()
     gp = call.untri_scores(dump_p)
     gm = call.untri_scores(dump_m)
@@ -207,13 +233,13 @@ def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n
             oracle_ms.append(torch.zeros(q.shape[1], 0, 0))
             continue
         mk_o = O.pool_k(k[s0:s1], block)
-        ulp, diff, worst = pool_errors(mk_gpu[tile[b]:tile[b + 1]], mk_o)
+        ulp, diff, worst = pool_errors(mk_gpu[stile[b]:stile[b + 1]], mk_o)
         rep.pool_ulp = max(rep.pool_ulp, ulp)
         rep.pool_mismatch += diff
         if diff:
             rep.notes.append(f"pooled K differs from the oracle's, seq {b}: {worst}")
         # scores from the GPU's own pooled K (isolates the score kernel)
-        p_o, m_o = O.block_score(q[s0:s1], mk_gpu[tile[b]:tile[b + 1]], block)
+        p_o, m_o = O.block_score(q[s0:s1], mk_gpu[stile[b]:stile[b + 1]], block)
         nb = p_o.shape[-1]
         tril = torch.tril(torch.ones(nb, nb, dtype=torch.bool)).expand_as(p_o)
         dm = (gm[b][tril] - m_o[tril]).abs() / m_o[tril].abs().clamp_min(1.0)
@@ -245,7 +271,8 @@ def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n
                 continue
             want = O.select_from_scores(oracle_ps[b], oracle_ms[b], native, alpha, sink, window,
                                         last_n, min_budget)
-            rep.sel_from_oracle_scores_mismatch += int((sel2[b] != want).sum())
+            rep.sel_from_oracle_scores_mismatch += int(
+                (sel2[b] != expand_sel(want, ratio, sel2[b].shape[-1])).sum())
         # restore the GPU's own selection for the attention stage
         call.search()
 
@@ -277,7 +304,7 @@ def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n
         if attn_rows is not None:
             # the oracle saw sampled rows only: every row against the closed
             # form on the GPU, from the same lists, under the same bars
-            fmax, fmean, rows = every_row_vs_closed_form(call, od, block=block)
+            fmax, fmean, rows = every_row_vs_closed_form(call, od, block=block // ratio)
             rep.notes.append(f"closed form, every row: {rows} rows, max {fmax:.2e} "
                              f"mean {fmean:.2e}")
             rep.out_max_abs = max(rep.out_max_abs, fmax)

@@ -111,6 +111,23 @@ def test_split_partials_stay_within_their_byte_budget(B, S, hq, d, block):
         assert L.split_blocks > 0  # a single 4K sequence still splits its dense rows
 
 
+def test_layout_block_256_plans_in_128_token_blocks():
+    # block_size 256 selects 256-token blocks over a 128-token plan: the
+    # items, counts, lists and pooled-key slots are those of block 128
+    rc256, L256 = _layout(_problem(block_size=256))
+    rc128, L128 = _layout(_problem(block_size=128))
+    assert rc256 == rc128 == _lib.FP_OK
+    for f in ("nb_max", "nb_sum_cap", "tri_cap", "mk_off", "cnt_off", "rowrec_off", "idx_off",
+              "total_bytes"):
+        assert getattr(L256, f) == getattr(L128, f), f
+    # up to 8192 plan blocks per sequence: 1,048,576 tokens
+    rc, _ = _layout(_problem(block_size=256, max_seq_len=8192 * 128, total_tokens=8192 * 128,
+                             batch=1))
+    assert rc == _lib.FP_OK
+    rc, _ = _layout(_problem(block_size=256, max_seq_len=8192 * 128 + 1, batch=1))
+    assert rc == _lib.FP_E_INVALID_ARG
+
+
 @pytest.mark.parametrize("field,value,code", [
     ("dtype", _lib.FP_DTYPE_F32, _lib.FP_E_UNSUPPORTED),
     ("head_dim", 96, _lib.FP_E_UNSUPPORTED),
@@ -176,7 +193,8 @@ def test_layout_bounds_block_64():
 @pytest.mark.parametrize("field,value,code", [
     ("dtype", 7, _lib.FP_E_UNSUPPORTED),
     ("head_dim", 96, _lib.FP_E_UNSUPPORTED),
-    ("block_size", 256, _lib.FP_E_UNSUPPORTED),
+    ("head_dim", 256, _lib.FP_E_UNSUPPORTED),
+    ("block_size", 512, _lib.FP_E_UNSUPPORTED),
     ("block_size", 96, _lib.FP_E_UNSUPPORTED),
     ("num_kv_heads", 3, _lib.FP_E_INVALID_ARG),
     ("batch", 0, _lib.FP_E_INVALID_ARG),

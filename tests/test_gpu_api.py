@@ -263,4 +263,8 @@ def test_error_paths():
                                   q96.clone(), cu, T, 0.1)
     with pytest.raises(NotImplementedError):
         flash_prefill_varlen_func(qb, qb[:, :1].contiguous(), qb[:, :1].contiguous(), qb.clone(),
-                                  cu, T, 0.1, block_size=256)
+                                  cu, T, 0.1, block_size=512)
+    q256 = torch.zeros(T, 4, 256, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(NotImplementedError):  # head_dim 256 is not built
+        flash_prefill_varlen_func(q256, q256[:, :1].contiguous(), q256[:, :1].contiguous(),
+                                  q256.clone(), cu, T, 0.1)
