@@ -244,6 +244,159 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
   }
 }
 
+// d = 256: one selected block in two passes of KP = 2 key tiles (64 keys)
+// each: S, the online softmax and O += V^T.P^T per pass, so that a pass's S
+// and P (32 + 16 registers) sit beside the 128 output accumulators and the
+// 64 query-operand registers of a wave. This is the online softmax over
+// 64-key tiles (the reference's other K_TILE_SIZE), a rounding-level
+// difference from one 128-key tile. The K refill follows the last pass's S,
+// the V refill the last pass's P.V; the V wait precedes the first pass's P.V.
+template <typename T, int D, int BLK, bool DIAG>
+__device__ __forceinline__ void attn_block_2pass(AttnState<T, D>& st, const typename T::vec8* qb,
+                                                 const uint4* sk, uint4* sk_w,
+                                                 const uint16_t* sv16, uint4* sv_w,
+                                                 const uint16_t* kbase, const uint16_t* vbase,
+                                                 int64_t kst, int64_t vst,
+                                                 const TileLanes<D, BLK, BLK / 32>& tk,
+                                                 const TileLanes<D, BLK, BLK / 32>& tv, int jn,
+                                                 const int32_t* pf, int& jpf, int L, float c,
+                                                 bool first, int w, int lane) {
+  constexpr int CH = D / 8;
+  constexpr int KS = D / 16;
+  constexpr int DT = D / 32;
+  constexpr int KT = BLK / 32;  // 32-key tiles of S^T per block
+  constexpr int KP = 2;         // key tiles per pass
+  constexpr int NP = KT / KP;   // passes
+  constexpr int NW = BLK / 32;
+  static_assert(KT % KP == 0, "whole passes");
+  const int half = lane >> 5, l32 = lane & 31;
+  const int qrow = 32 * w + l32;
+  const int live = DIAG ? w + 1 : KT;
+  const int g16 = lane >> 4, i16 = lane & 15;
+  const int tr_row = 4 * (g16 >> 1) + (i16 >> 2);
+  const int tr_col = 16 * (g16 & 1) + 4 * (i16 & 3);
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    // the pass's live tiles (diagonal block: wave w sees tiles 0 .. w)
+    const int live_p = DIAG ? min(max(live - p * KP, 0), KP) : KP;
+    f32x16 s[KP];
+#pragma unroll
+    for (int t = 0; t < KP; ++t) s[t] = f32x16{};
+    if constexpr (!DIAG) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int t = 0; t < KP; ++t) {
+          const int r = 32 * (p * KP + t) + l32;
+          const uint4 kop = sk[r * CH + ((2 * ks + half) ^ swz<D>(r))];
+          s[t] = T::mfma32(as_vec8<T>(kop), qb[ks], s[t]);
+        }
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kReadAhead, 0);
+#pragma unroll
+      for (int k = 0; k < KS * KP - kReadAhead; ++k) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, kReadAhead, 0);
+    } else {
+#pragma unroll
+      for (int t = 0; t < KP; ++t) {
+        if (t >= live_p) continue;
+        const int r = 32 * (p * KP + t) + l32;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const uint4 kop = sk[r * CH + ((2 * ks + half) ^ swz<D>(r))];
+          s[t] = T::mfma32(as_vec8<T>(kop), qb[ks], s[t]);
+        }
+      }
+    }
+    if (p == NP - 1) {
+      lds_barrier();  // every wave is done with the K buffer
+      if (jn >= 0) issue_tile<D, BLK, NW>(sk_w, kbase, kst, tk, jn, L, w, lane);
+      jpf = sld(pf);
+    }
+    if (DIAG && live_p == 0) continue;  // wave-uniform: no key of this pass is visible
+
+    if constexpr (DIAG) {  // key > query is masked on the diagonal block
+#pragma unroll
+      for (int t = 0; t < KP; ++t) {
+        const int t4 = p * KP + t;
+        if (t4 < w) continue;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = 32 * t4 + 8 * (v >> 2) + 4 * half + (v & 3);
+          if (t4 > w || key > qrow) s[t][v] = -INFINITY;
+        }
+      }
+    }
+    // conditional rescaling as in attn_block, per pass
+    uint32_t pk[KP][8];
+    float ps = 0.0f;
+    bool move = first && p == 0;
+    if (!move) {
+      ps = exp_pack<T, KP>(s, st.m_run, c, live_p, pk);
+      move = __ballot(!(ps <= kRescaleSum)) != 0;
+    }
+    if (move) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < KP; ++t)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[t][v]);
+      const float m_new = fmaxf(st.m_run, pair32_max(mx) * c);
+      float alpha = __builtin_amdgcn_exp2f(st.m_run - m_new);
+      if (alpha != alpha) alpha = 1.0f;
+      st.l_part *= alpha;
+      st.m_run = m_new;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) st.o[dt][v] *= alpha;
+      ps = exp_pack<T, KP>(s, st.m_run, c, live_p, pk);
+    }
+    st.l_part += ps;
+
+    if (p == 0) vm_barrier<0>();  // V of this block has landed (no K refill issued yet)
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int u = 0; u < 2 * KP; ++u) {
+      const int t = u >> 1, hh = u & 1;
+      if (DIAG && t >= live_p) continue;
+      const uint4 pu = make_uint4(pk[t][4 * hh], pk[t][4 * hh + 1], pk[t][4 * hh + 2],
+                                  pk[t][4 * hh + 3]);
+      const typename T::vec8 pb = __builtin_bit_cast(typename T::vec8, pu);
+      const int r1 = 16 * (2 * KP * p + u) + tr_row;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int x = 32 * dt + tr_col;
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4*)(sv16 + tile_elem<D>(r1, x)));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4*)(sv16 + tile_elem<D>(r1 + 8, x)));
+        const uint2 lo2 = __builtin_bit_cast(uint2, lo), hi2 = __builtin_bit_cast(uint2, hi);
+        const uint4 va = make_uint4(lo2.x, lo2.y, hi2.x, hi2.y);
+        st.o[dt] = T::mfma32(as_vec8<T>(va), pb, st.o[dt]);
+      }
+    }
+    if constexpr (!DIAG) {
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kReadAhead, 0);
+#pragma unroll
+      for (int k = 0; k < 2 * KP * DT - kReadAhead; ++k) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, kReadAhead, 0);
+    }
+    __builtin_amdgcn_s_setprio(0);
+  }
+  if (jn >= 0) {
+    // every wave is done with the V buffer, and every wave's part of the next
+    // block's K (the only load in flight) has landed
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    issue_tile<D, BLK, NW>(sv_w, vbase, vst, tv, jn, L, w, lane);
+  }
+}
+
 // Flash-decoding merge of a split row's chunk partials into its output rows:
 // m = max_c m_c, w_c = exp2(m_c - m), O = sum_c w_c acc_c / sum_c w_c l_c,
 // with the chunks taken in order (the arithmetic of k_merge, so either path
@@ -467,13 +620,24 @@ __device__ __forceinline__ bool attn_slot(const Args& a, int slot, int t, Tail t
   // (entry ncnt - 1 past the end of the list; not used then)
   for (int n = 0; n < nplain; ++n) {
     const int jn = n + 1 < ncnt ? min(max(jraw, 0), i) : -1;
-    attn_block<T, D, BLK, false>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv, jn,
-                            list + min(n + 2, ncnt - 1), jraw, L, c, n == 0, w, lane);
+    if constexpr (D > 128) {
+      attn_block_2pass<T, D, BLK, false>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk,
+                                         tv, jn, list + min(n + 2, ncnt - 1), jraw, L, c, n == 0,
+                                         w, lane);
+    } else {
+      attn_block<T, D, BLK, false>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv,
+                                   jn, list + min(n + 2, ncnt - 1), jraw, L, c, n == 0, w, lane);
+    }
   }
   if (has_diag) {
     int unused;
-    attn_block<T, D, BLK, true>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv, -1,
-                           list, unused, L, c, nplain == 0, w, lane);
+    if constexpr (D > 128) {
+      attn_block_2pass<T, D, BLK, true>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk,
+                                        tv, -1, list, unused, L, c, nplain == 0, w, lane);
+    } else {
+      attn_block<T, D, BLK, true>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv, -1,
+                                  list, unused, L, c, nplain == 0, w, lane);
+    }
   }
 
   tail();
@@ -537,7 +701,10 @@ __device__ __forceinline__ bool attn_slot(const Args& a, int slot, int t, Tail t
 // BLK = 128: 4 waves, 64 KB of LDS (d = 128), two workgroups per CU;
 // BLK = 64: 2 waves, 32 KB, four workgroups per CU. Either way two waves per
 // SIMD (the second launch bound is waves per execution unit), i.e. at most
-// 256 registers per wave.
+// 256 registers per wave. At d = 256 (two passes per block) the output
+// accumulators take 128 registers and the query operands 64: a wave runs
+// alone on its SIMD (up to 512 registers, VGPRs and AGPRs), one workgroup
+// per CU at BLK = 128 (128 KB of LDS), two at BLK = 64.
 //
 // PERSIST = false: one workgroup per slot (grid = total_slots), in slot order.
 // PERSIST = true: a resident grid (a multiple of 8 workgroups, as many as fit)
@@ -548,7 +715,7 @@ __device__ __forceinline__ bool attn_slot(const Args& a, int slot, int t, Tail t
 // total_slots ends the workgroup's loop; the last claim of a queue empties it
 // for the next launch.
 template <typename T, int D, int BLK, bool PERSIST>
-__global__ __launch_bounds__(2 * BLK, 2) void k_attn(AttnArgs a) {
+__global__ __launch_bounds__(2 * BLK, D > 128 ? 1 : 2) void k_attn(AttnArgs a) {
   // The arguments are read from the kernel-argument segment through a
   // pointer (made opaque on every pass of the persistent loop, so that the
   // compiler reloads them per slot with scalar loads instead of keeping ~70 of
@@ -691,21 +858,21 @@ hipError_t launch_merge_t(const AttnArgs& a, int block, hipStream_t s) {
 
 hipError_t launch_merge(const AttnArgs& a, int dtype, int head_dim, int block, hipStream_t s) {
   if (a.unit_slots <= 0 || dtype == FP_DTYPE_F32) return hipSuccess;
-  if (dtype == FP_DTYPE_BF16)
-    return head_dim == 128 ? launch_merge_t<BF16, 128>(a, block, s)
-                           : launch_merge_t<BF16, 64>(a, block, s);
-  return head_dim == 128 ? launch_merge_t<F16, 128>(a, block, s)
-                         : launch_merge_t<F16, 64>(a, block, s);
+  return with_head_dim(head_dim, [&](auto dc) {
+    constexpr int D = decltype(dc)::value;
+    return dtype == FP_DTYPE_BF16 ? launch_merge_t<BF16, D>(a, block, s)
+                                  : launch_merge_t<F16, D>(a, block, s);
+  });
 }
 
 hipError_t launch_attn(const AttnArgs& a, int dtype, int head_dim, int block, int64_t grid,
                        bool persist, hipStream_t s) {
   if (grid <= 0) return hipSuccess;
-  if (dtype == FP_DTYPE_BF16)
-    return head_dim == 128 ? launch_attn_t<BF16, 128>(a, block, grid, persist, s)
-                           : launch_attn_t<BF16, 64>(a, block, grid, persist, s);
-  return head_dim == 128 ? launch_attn_t<F16, 128>(a, block, grid, persist, s)
-                         : launch_attn_t<F16, 64>(a, block, grid, persist, s);
+  return with_head_dim(head_dim, [&](auto dc) {
+    constexpr int D = decltype(dc)::value;
+    return dtype == FP_DTYPE_BF16 ? launch_attn_t<BF16, D>(a, block, grid, persist, s)
+                                  : launch_attn_t<F16, D>(a, block, grid, persist, s);
+  });
 }
 
 }  // namespace fp

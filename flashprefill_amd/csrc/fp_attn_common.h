@@ -47,10 +47,14 @@ __device__ __forceinline__ X sld(const X* p) {
   return x;
 }
 
-// chunk swizzle of row r in a 128 x D tile (D/8 chunks of 16 bytes per row)
+// chunk swizzle of row r in a 128 x D tile (D/8 chunks of 16 bytes per row):
+// rows of 16 or 32 chunks (d = 128, 256) permute the low 4 chunk bits by the
+// row's low 4 bits (conflict free for the K operand reads and the transposing
+// V reads alike, since a row is a whole number of 256-byte bank cycles), rows
+// of 8 chunks (d = 64) the low 3 bits
 template <int D>
 __device__ __forceinline__ int swz(int r) {
-  if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+  if constexpr (D >= 128) return ((r & 3) << 2) | ((r >> 2) & 3);
   else return (r >> 1) & 7;
 }
 
@@ -151,7 +155,7 @@ struct TileLanes {
   static constexpr int CH = D / 8;            // chunks per row
   static constexpr int RPW = 64 / CH;         // rows per wave instruction
   static constexpr int NI = R * CH / 64 / NW; // instructions per wave per tile
-  static constexpr int PER = D == 128 ? 4 : 2;  // period of swz over the slice index
+  static constexpr int PER = D == 256 ? 8 : D == 128 ? 4 : 2;  // period of swz over the slice index
   static_assert(NI >= 1 && NI % PER == 0, "every wave's first slice must start a swizzle period");
   uint32_t off[PER];                          // per-lane byte offsets
   __device__ __forceinline__ void init(int64_t stride, int w, int lane) {

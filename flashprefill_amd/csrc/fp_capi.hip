@@ -53,8 +53,15 @@ int validate(const fp_problem* p) {
   if (!p->q || !p->k || !p->v || !p->o) return fail(FP_E_INVALID_ARG, "q/k/v/o must be non-NULL");
   if (p->dtype != FP_DTYPE_BF16 && p->dtype != FP_DTYPE_F16 && p->dtype != FP_DTYPE_F32)
     return fail(FP_E_UNSUPPORTED, "dtype %d unsupported (bf16, fp16 or fp32)", p->dtype);
-  if (p->head_dim != 64 && p->head_dim != 128)
-    return fail(FP_E_UNSUPPORTED, "head_dim %d unsupported (64 or 128)", p->head_dim);
+  if (p->head_dim != 64 && p->head_dim != 128 && p->head_dim != 256)
+    return fail(FP_E_UNSUPPORTED, "head_dim %d unsupported (64, 128 or 256)", p->head_dim);
+  // head_dim 256 is built for bf16 / fp16 at blocks of 64 and 128: the fp32
+  // kernels' padded 128-row tiles (133 KB each) and a 256-row, d = 256 query
+  // block (128 KB) do not fit the 160 KB of LDS beside the rest
+  if (p->head_dim == 256 && p->dtype == FP_DTYPE_F32)
+    return fail(FP_E_UNSUPPORTED, "head_dim 256 is supported for bf16 and fp16 inputs, not fp32");
+  if (p->head_dim == 256 && p->block_size == 256)
+    return fail(FP_E_UNSUPPORTED, "head_dim 256 is supported at block_size 64 and 128, not 256");
   if (p->block_size != 64 && p->block_size != 128 && p->block_size != 256)
     return fail(FP_E_UNSUPPORTED, "block_size %d unsupported (64, 128 or 256)", p->block_size);
   if (p->num_q_heads < 1 || p->num_kv_heads < 1 || p->num_q_heads % p->num_kv_heads)
@@ -181,9 +188,9 @@ fp::SeqTables tables(const fp_ws_layout& L, void* ws) {
 
 // Workgroups of the attention kernel resident on the current device at once:
 // two per CU at block 128 (64 KB of LDS, 4 waves), four at block 64 (32 KB,
-// 2 waves), rounded up to a multiple of the 8 XCDs. The CU count is read once
-// per device.
-int resident_attn_workgroups(int block, int64_t* out) {
+// 2 waves), half that at d = 256 (one wave per SIMD, twice the LDS), rounded
+// up to a multiple of the 8 XCDs. The CU count is read once per device.
+int resident_attn_workgroups(int block, int head_dim, int64_t* out) {
   constexpr int kDevs = 64;
   static std::mutex mu;
   static int cus[kDevs] = {};
@@ -199,7 +206,7 @@ int resident_attn_workgroups(int block, int64_t* out) {
     if (n < 1) return fail(FP_E_LAUNCH, "device reports %d CUs", n);
     cus[dev] = n;
   }
-  const int64_t per_cu = block == 128 ? 2 : 4;
+  const int64_t per_cu = (block == 128 ? 2 : 4) / (head_dim == 256 ? 2 : 1);
   *out = (cus[dev] * per_cu + 7) / 8 * 8;
   return FP_OK;
 }
@@ -382,7 +389,7 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
     // one workgroup per slot (4K, 2.5 slots per workgroup: the persistent
     // loop's per-slot claim costs more than it saves, +3 %).
     int64_t resident = 0;
-    const int rc = resident_attn_workgroups(blk, &resident);
+    const int rc = resident_attn_workgroups(blk, p->head_dim, &resident);
     if (rc != FP_OK) return rc;
     const bool persist = a.total_slots >= 4 * resident;
     const int64_t grid = persist ? resident : a.total_slots;
@@ -517,8 +524,8 @@ int fp_rope_qk(const fp_rope_args* a, void* stream) {
   if (!a) return fail(FP_E_INVALID_ARG, "rope args are NULL");
   if (a->dtype != FP_DTYPE_BF16 && a->dtype != FP_DTYPE_F16)
     return fail(FP_E_UNSUPPORTED, "rope: dtype %d unsupported (bf16 or fp16)", a->dtype);
-  if (a->head_dim != 64 && a->head_dim != 128)
-    return fail(FP_E_UNSUPPORTED, "rope: head_dim %d unsupported (64 or 128)", a->head_dim);
+  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256)
+    return fail(FP_E_UNSUPPORTED, "rope: head_dim %d unsupported (64, 128 or 256)", a->head_dim);
   if (a->num_tokens < 0 || a->num_q_heads < 0 || a->num_kv_heads < 0 || a->num_positions < 1)
     return fail(FP_E_INVALID_ARG, "rope: negative sizes or an empty table");
   if (a->num_tokens == 0) return FP_OK;

@@ -3,6 +3,8 @@
 // or workspace; strides are in elements.
 #pragma once
 
+#include <type_traits>
+
 #include "fp_common.h"
 
 namespace fp {
@@ -133,6 +135,15 @@ struct RopeArgs {
   const void* k_norm;
   float eps;
 };
+
+// f(std::integral_constant<int, D>{}) for the head dim D of the 16-bit
+// kernels' instantiations (64, 128, 256; the C ABI rejects any other)
+template <typename F>
+auto with_head_dim(int head_dim, F&& f) {
+  if (head_dim == 256) return f(std::integral_constant<int, 256>{});
+  if (head_dim == 128) return f(std::integral_constant<int, 128>{});
+  return f(std::integral_constant<int, 64>{});
+}
 
 hipError_t launch_plan(const PlanArgs& a, hipStream_t s);
 hipError_t launch_rope(const RopeArgs& a, int dtype, hipStream_t s);

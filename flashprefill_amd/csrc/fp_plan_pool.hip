@@ -530,13 +530,12 @@ hipError_t launch_plan_pool(const PlanArgs& pa, const PoolArgs& a, int dtype, in
                             hipStream_t s) {
   // one workgroup per (key block, kv head) of the capacity, plus the table writer
   const dim3 g(static_cast<unsigned>(a.nb_sum_cap * a.Hkv + 1)), blk(256);
-  if (dtype == FP_DTYPE_BF16) {
-    if (head_dim == 128) hipLaunchKernelGGL((k_plan_pool<BF16, 128>), g, blk, 0, s, pa, a);
-    else hipLaunchKernelGGL((k_plan_pool<BF16, 64>), g, blk, 0, s, pa, a);
-  } else {
-    if (head_dim == 128) hipLaunchKernelGGL((k_plan_pool<F16, 128>), g, blk, 0, s, pa, a);
-    else hipLaunchKernelGGL((k_plan_pool<F16, 64>), g, blk, 0, s, pa, a);
-  }
+  with_head_dim(head_dim, [&](auto dc) {
+    constexpr int D = decltype(dc)::value;
+    if (dtype == FP_DTYPE_BF16) hipLaunchKernelGGL((k_plan_pool<BF16, D>), g, blk, 0, s, pa, a);
+    else hipLaunchKernelGGL((k_plan_pool<F16, D>), g, blk, 0, s, pa, a);
+    return 0;
+  });
   return hipGetLastError();
 }
 
@@ -546,12 +545,13 @@ hipError_t launch_pool(const PoolArgs& a, int dtype, int head_dim, int64_t grid,
   const dim3 g(static_cast<unsigned>(grid * a.Hkv)), blk(256);
   if (dtype == FP_DTYPE_F32) {
     hipLaunchKernelGGL(k_pool_f32, g, blk, 0, s, a, head_dim);
-  } else if (dtype == FP_DTYPE_BF16) {
-    if (head_dim == 128) hipLaunchKernelGGL((k_pool<BF16, 128>), g, blk, 0, s, a);
-    else hipLaunchKernelGGL((k_pool<BF16, 64>), g, blk, 0, s, a);
   } else {
-    if (head_dim == 128) hipLaunchKernelGGL((k_pool<F16, 128>), g, blk, 0, s, a);
-    else hipLaunchKernelGGL((k_pool<F16, 64>), g, blk, 0, s, a);
+    with_head_dim(head_dim, [&](auto dc) {
+      constexpr int D = decltype(dc)::value;
+      if (dtype == FP_DTYPE_BF16) hipLaunchKernelGGL((k_pool<BF16, D>), g, blk, 0, s, a);
+      else hipLaunchKernelGGL((k_pool<F16, D>), g, blk, 0, s, a);
+      return 0;
+    });
   }
   return hipGetLastError();
 }

@@ -87,13 +87,12 @@ hipError_t launch_rope(const RopeArgs& a, int dtype, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
   const int64_t want = (rows + 15) / 16;  // 16 rows per workgroup of 256 threads
   const dim3 g(static_cast<unsigned>(want < 65536 ? want : 65536)), b(256);
-  if (dtype == FP_DTYPE_BF16) {
-    if (a.head_dim == 128) hipLaunchKernelGGL((k_rope<BF16, 128>), g, b, 0, s, a);
-    else hipLaunchKernelGGL((k_rope<BF16, 64>), g, b, 0, s, a);
-  } else {
-    if (a.head_dim == 128) hipLaunchKernelGGL((k_rope<F16, 128>), g, b, 0, s, a);
-    else hipLaunchKernelGGL((k_rope<F16, 64>), g, b, 0, s, a);
-  }
+  with_head_dim(a.head_dim, [&](auto dc) {
+    constexpr int D = decltype(dc)::value;
+    if (dtype == FP_DTYPE_BF16) hipLaunchKernelGGL((k_rope<BF16, D>), g, b, 0, s, a);
+    else hipLaunchKernelGGL((k_rope<F16, D>), g, b, 0, s, a);
+    return 0;
+  });
   return hipGetLastError();
 }
 

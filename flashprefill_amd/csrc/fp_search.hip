@@ -261,7 +261,7 @@ __device__ __forceinline__ void select_row(float* pl, float* ml, int n, int i, i
 // MFMA A-operand reads of 16 rows x one chunk column on the 64-bank LDS)
 template <int D>
 __device__ __forceinline__ int qswz(int r) {
-  if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
+  if constexpr (D >= 128) return ((r & 3) << 2) | ((r >> 2) & 3);
   else return (r >> 1) & 7;
 }
 
@@ -272,10 +272,11 @@ constexpr size_t search_q_bytes() { return FROM_SCORES ? kSelectScratch : BLK * 
 // BLK is the selection block: 64 or 128 (the plan's block, ratio 1), or 256
 // over a 128-token plan (ratio 2).
 template <typename T, int D, int BLK, bool FROM_SCORES>
-__global__ __launch_bounds__(256, BLK > 128 ? 2 : 4) void k_search(SearchArgs a) {
+__global__ __launch_bounds__(256, (BLK > 128 || D > 128) ? 2 : 4) void k_search(SearchArgs a) {
   // 4 workgroups per CU at BLK = 128: 4 x (32 KB query block + 2 x 4 KB p / m
   // at 1024 blocks) = 160 KB of LDS, and at most 128 VGPRs per wave (BLK =
-  // 256: a 64 KB query block and 8 row groups of accumulators, two per CU)
+  // 256: a 64 KB query block and 8 row groups of accumulators; d = 256: a 64
+  // KB query block and 16 k-steps of key operands; two per CU)
   constexpr int RG = BLK / 32;  // 32-row groups of the query block
   constexpr int RATIO = BLK > 128 ? 2 : 1;  // selection blocks per plan block
   extern __shared__ uint4 dyn4[];
@@ -707,11 +708,11 @@ hipError_t launch_search(const SearchArgs& args, int dtype, int head_dim, int bl
     return head_dim == 128 ? launch_search_f32_d<128>(a, block, grid, s)
                            : launch_search_f32_d<64>(a, block, grid, s);
   }
-  if (dtype == FP_DTYPE_BF16)
-    return head_dim == 128 ? launch_search_d<BF16, 128>(a, block, grid, from_scores, s)
-                           : launch_search_d<BF16, 64>(a, block, grid, from_scores, s);
-  return head_dim == 128 ? launch_search_d<F16, 128>(a, block, grid, from_scores, s)
-                         : launch_search_d<F16, 64>(a, block, grid, from_scores, s);
+  return with_head_dim(head_dim, [&](auto dc) {
+    constexpr int D = decltype(dc)::value;
+    return dtype == FP_DTYPE_BF16 ? launch_search_d<BF16, D>(a, block, grid, from_scores, s)
+                                  : launch_search_d<F16, D>(a, block, grid, from_scores, s);
+  });
 }
 
 }  // namespace fp

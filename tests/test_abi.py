@@ -193,7 +193,7 @@ def test_layout_bounds_block_64():
 @pytest.mark.parametrize("field,value,code", [
     ("dtype", 7, _lib.FP_E_UNSUPPORTED),
     ("head_dim", 96, _lib.FP_E_UNSUPPORTED),
-    ("head_dim", 256, _lib.FP_E_UNSUPPORTED),
+    ("head_dim", 512, _lib.FP_E_UNSUPPORTED),
     ("block_size", 512, _lib.FP_E_UNSUPPORTED),
     ("block_size", 96, _lib.FP_E_UNSUPPORTED),
     ("num_kv_heads", 3, _lib.FP_E_INVALID_ARG),

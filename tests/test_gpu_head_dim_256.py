@@ -1,0 +1,88 @@
+"""GPU parity at head_dim 256 (bf16 / fp16; the reference takes any power-of-two
+head dim, tl.arange(0, D_HEAD) at ops/flashprefill_varlen_func.py:68).
+
+At d = 256 the attention kernel walks each 128-key block in two passes of 64
+keys (the online softmax over 64-key tiles, as the oracle computes it with
+k_tile 64) with one wave per SIMD; pooling, scoring and selection are the
+d = 128 kernels' at 16 k-steps. Bars as in test_gpu_parity.py.
+"""
+
+import pytest
+import torch
+
+from flashprefill_amd import flash_prefill_varlen_func, synth
+from oracle import flashprefill_oracle as O
+from tests._parity import OUT_MAX_ABS, OUT_MEAN_ABS, assert_pool, run_stages
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(rep, max_flip_frac=2e-3):
+    print(f"\n  pool_ulp={rep.pool_ulp} pool_mismatch={rep.pool_mismatch} "
+          f"m_rel={rep.m_max_rel:.2e} p_rel={rep.p_max_rel:.2e} "
+          f"sel_mismatch(gpu scores)={rep.sel_from_gpu_scores_mismatch} "
+          f"sel_mismatch(oracle scores)={rep.sel_from_oracle_scores_mismatch} "
+          f"e2e_flips={rep.e2e_flips}/{rep.cells} density={rep.density:.3f} "
+          f"out_max={rep.out_max_abs:.2e} out_mean={rep.out_mean_abs:.2e} {rep.notes}",
+          flush=True)
+    assert_pool(rep)
+    assert rep.m_max_rel < 1e-4
+    assert rep.p_max_rel < 1e-3
+    assert rep.sel_from_gpu_scores_mismatch == 0
+    assert rep.sel_from_oracle_scores_mismatch == 0
+    assert rep.e2e_flips <= max(2, max_flip_frac * rep.cells)
+    assert rep.out_max_abs <= OUT_MAX_ABS
+    assert rep.out_mean_abs <= OUT_MEAN_ABS
+
+
+@pytest.mark.parametrize("dtype,block,native", [(torch.bfloat16, 128, False),
+                                                (torch.float16, 64, True)])
+def test_ragged_structured(dtype, block, native):
+    lens = (3000, 1300, 129, 1)
+    spec = synth.SynthSpec(seq_lens=lens, num_q_heads=8, num_kv_heads=2, head_dim=256,
+                           dtype=dtype, seed=41)
+    q, k, v, cu = synth.make_inputs(spec)
+    print(f"\n  d256 {dtype} block {block} native={native} lens={lens}", flush=True)
+    rep = run_stages(q, k, v, cu.tolist(), max(lens), alpha=0.5, sink=1, window=2,
+                     native=native, block=block)
+    assert rep.density < 0.9
+    _check(rep)
+
+
+def test_persistent_grid_every_row():
+    # 16K tokens x 16 heads: the persistent attention grid (one workgroup per
+    # CU at d = 256) and split dense rows; sampled rows against the oracle,
+    # every row against the closed form
+    spec = synth.SynthSpec(seq_lens=(16384,), num_q_heads=16, num_kv_heads=4, head_dim=256,
+                           seed=42)
+    q, k, v, cu = synth.make_inputs(spec)
+    rows = {0: [(0, 127), (5, 64), (15, 0)]}
+    print("\n  d256 16K persistent", flush=True)
+    rep = run_stages(q, k, v, cu.tolist(), 16384, alpha=0.18, attn_rows=rows)
+    assert rep.full_rows > 0
+    _check(rep)
+
+
+def test_public_entry_point():
+    dev = torch.device("cuda:0")
+    lens = [1500, 77]
+    g = torch.Generator().manual_seed(43)
+    T = sum(lens)
+    q = torch.randn(T, 4, 256, generator=g).to(torch.bfloat16)
+    k = torch.randn(T, 1, 256, generator=g).to(torch.bfloat16)
+    v = torch.randn(T, 1, 256, generator=g).to(torch.bfloat16)
+    cu = [0, lens[0], T]
+    print("\n  d256 public varlen", flush=True)
+    o = torch.empty_like(q, device=dev)
+    flash_prefill_varlen_func(q.to(dev), k.to(dev), v.to(dev), o,
+                              torch.tensor(cu, dtype=torch.int32, device=dev), max(lens), 0.18)
+    torch.cuda.synchronize()
+    # the GPU walks 64-key tiles at d = 256
+    res = O.flash_prefill_varlen_func(q, k, v, cu, max(lens), 0.18, with_output=False)
+    ref = torch.zeros_like(q)
+    for b in range(len(lens)):
+        s0, s1 = cu[b], cu[b + 1]
+        ref[s0:s1] = O.sparse_attention(q[s0:s1], k[s0:s1], v[s0:s1], res.traces[b].sel, 128, 64)
+    d = (o.cpu().float() - ref.float()).abs()
+    print(f"  out_max={float(d.max()):.2e} out_mean={float(d.mean()):.2e}", flush=True)
+    assert float(d.max()) <= OUT_MAX_ABS and float(d.mean()) <= OUT_MEAN_ABS
