@@ -43,7 +43,7 @@ extern "C" {
 
 #define FP_OK 0
 #define FP_E_INVALID_ARG (-1)   /* shapes, strides, alignment or scalars out of range */
-#define FP_E_UNSUPPORTED (-2)   /* valid for the reference but not built here (e.g. head_dim 256) */
+#define FP_E_UNSUPPORTED (-2)   /* valid for the reference but not built here (e.g. head_dim 32) */
 #define FP_E_LAUNCH (-3)        /* a HIP launch or runtime call failed */
 
 #define FP_DTYPE_BF16 0
@@ -79,7 +79,7 @@ typedef struct fp_problem {
     int64_t total_tokens;  /* T = number of rows of q/k/v/o */
     int32_t num_q_heads;
     int32_t num_kv_heads;
-    int32_t head_dim;      /* 64 or 128 */
+    int32_t head_dim;      /* 64, 128 or 256 (256: bf16 / fp16 at block_size 64 or 128) */
     int32_t dtype;         /* FP_DTYPE_BF16, FP_DTYPE_F16 or FP_DTYPE_F32 */
     int32_t block_size;    /* 64, 128 or 256 (256: 256-token selection blocks over a
                               128-token plan, lists and attention; see below) */
