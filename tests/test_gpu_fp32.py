@@ -36,11 +36,14 @@ def _check(rep, max_flip_frac=2e-3):
     assert rep.out_mean_abs <= OUT_MEAN_ABS_F32
 
 
-@pytest.mark.parametrize("alpha", [0.18, 0.7])
+@pytest.mark.parametrize("alpha", [0.08, 0.12, 0.18, 0.7])
 def test_config1_full_size_fp32(alpha):
     # config 1 at its own size and dtype: 4096 tokens, 8 q / 2 kv heads,
     # d = 64, fp32, unscaled N(0, 1) with sinks and 16 stripe columns, seed 0;
-    # native normalisation as in the reference's native forward
+    # native normalisation as in the reference's native forward; the alphas
+    # of the reference's Qwen2 / Qwen3-MoE / Llama callers and its class
+    # default (ruler/models/qwen2.py:89, qwen3.py:126, llama.py:235,
+    # ops/flashprefill_native_forward.py:410)
     spec = synth.config1_spec(seed=0)
     q, k, v, cu = synth.make_inputs(spec)
     assert q.dtype == torch.float32
