@@ -9,7 +9,7 @@ from 12 on also vary the block size (64 / 128) and include fp32 inputs. The sequ
 so sink / window / last-n rules keep most blocks: these cases stress the
 edges (1-token and partial blocks, GQA ratios, d = 64, fp16, native mode,
 min_budget); sparse selection at length is covered by the structured 4K and
-128K tests. Four larger seeded cases (ragged batches of 19K-55K tokens from
+128K tests. A third set draws block sizes up to 256 and head dims up to 256. Four larger seeded cases (ragged batches of 19K-55K tokens from
 the structured synthetic distribution, sampled attention rows) are sized so
 that the attention stage runs as the persistent grid."""
 
@@ -78,6 +78,51 @@ def test_random_configuration(seed):
     q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
     print(f"\n  seed={seed} lens={lens} hq={hq} hkv={hkv} d={d} {dtype} block={block} {params} "
           f"{shape}", flush=True)
+    rep = run_stages(q, k, v, cu, max(lens), block=block, **params)
+    print(f"  flips={rep.e2e_flips}/{rep.cells} density={rep.density:.3f} "
+          f"out_max={rep.out_max_abs:.2e} out_mean={rep.out_mean_abs:.2e}", flush=True)
+    assert_pool(rep)
+    assert rep.m_max_rel < 1e-4
+    assert rep.p_max_rel < 1e-3
+    assert rep.sel_from_gpu_scores_mismatch == 0
+    assert rep.sel_from_oracle_scores_mismatch == 0
+    assert rep.e2e_flips <= max(2, 2e-3 * rep.cells)
+    f32 = dtype == torch.float32
+    assert rep.out_max_abs <= (OUT_MAX_ABS_F32 if f32 else OUT_MAX_ABS)
+    assert rep.out_mean_abs <= (OUT_MEAN_ABS_F32 if f32 else OUT_MEAN_ABS)
+
+
+def _wide_case(seed):
+    """Block sizes 64 / 128 / 256 and head dims 64 / 128 / 256 over the same
+    random edges (the supported combinations: head_dim 256 for 16-bit inputs at
+    blocks of 64 and 128)."""
+    lens, hq, hkv, _, _, params, shape, _ = _case(seed)
+    rnd = random.Random(seed * 7 + 3)
+    # (block, head_dim) in turn over the seeds
+    block, d = [(256, 128), (64, 256), (256, 64), (128, 256)][seed % 4]
+    dtype = rnd.choice([torch.bfloat16, torch.float16, torch.bfloat16, torch.float16, torch.float32])
+    if d == 256 and dtype == torch.float32:
+        dtype = torch.bfloat16
+    return lens, hq, hkv, d, dtype, params, shape, block
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_configuration_wide_blocks_and_head_dims(seed):
+    lens, hq, hkv, d, dtype, params, shape, block = _wide_case(3000 + seed)
+    g = torch.Generator().manual_seed(300 + seed)
+    T = sum(lens)
+    q = torch.randn(T, hq, d, generator=g) * shape["scale"]
+    k = torch.randn(T, hkv, d, generator=g) * shape["scale"]
+    v = torch.randn(T, hkv, d, generator=g)
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    if shape["sink"]:
+        for b in range(len(lens)):
+            k[cu[b]:min(cu[b] + 4, cu[b + 1])] *= 4.0
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
+    print(f"\n  seed={seed} lens={lens} hq={hq} hkv={hkv} d={d} {dtype} block={block} {params}",
+          flush=True)
     rep = run_stages(q, k, v, cu, max(lens), block=block, **params)
     print(f"  flips={rep.e2e_flips}/{rep.cells} density={rep.density:.3f} "
           f"out_max={rep.out_max_abs:.2e} out_mean={rep.out_mean_abs:.2e}", flush=True)
