@@ -397,20 +397,24 @@ __device__ __forceinline__ void attn_block_2pass(AttnState<T, D>& st, const type
   }
 }
 
-// Flash-decoding merge of a split row's chunk partials into its output rows:
+// Flash-decoding merge of a split row's chunk partials into its output rows,
+// inside the attention kernel (rows of at most kMaxInlineChunks chunks):
 // m = max_c m_c, w_c = exp2(m_c - m), O = sum_c w_c acc_c / sum_c w_c l_c,
 // with the chunks taken in order (the arithmetic of k_merge, so either path
 // gives the same bits). Threads: nt / BLK per query row (2 at BLK = 128 and
-// 64), each D / 2 dims in groups of 16; each round issues all of a group
-// pair's loads before using them.
+// 64), each D / 2 dims in rounds of 16; each round issues all of its loads
+// before using them (8 chunks x 16 dims: 128 registers, as many as the
+// attention itself leaves free). A loop over the chunks here, in any form
+// tried, made the compiler drop the LDS read-ahead schedule of the block loop
+// in the persistent kernel, so the chunks are unrolled.
 template <typename T, int D, int BLK, typename Args>
 __device__ __forceinline__ void merge_row(const Args& a, int h, int u0, int nc,
                                           const ItemRec& rec, int t) {
-  constexpr int MAXC = 4;          // chunks per split row (host policy)
+  constexpr int MAXC = kMaxInlineChunks;  // the host merges inline only up to this
   constexpr int NT = 2 * BLK;      // threads of the workgroup
   constexpr int TPR = NT / BLK;    // threads per query row
   constexpr int XT = D / TPR;      // dims per thread
-  constexpr int GP = 32;           // dims per round
+  constexpr int GP = 16;           // dims per round
   const int r = t / TPR;
   const int qg = rec.i * BLK + r;
   if (qg >= rec.L) return;
@@ -460,6 +464,89 @@ __device__ __forceinline__ void merge_row(const Args& a, int h, int u0, int nc,
       pk.y = pack2<T>(acc.z * rcp, acc.w * rcp);
       *reinterpret_cast<uint2*>(op + x0 + 4 * q) = pk;
     }
+  }
+}
+
+// The steps of k_merge (rows of up to kMaxChunks chunks), the same arithmetic
+// in the same chunk order as merge_row. A partial is S floats: acc[BLK][D],
+// then m[BLK], then l[BLK].
+
+// m and 1 / sum_c w_c l_c of query row r over the nc (<= kMaxChunks) partials
+// at p0
+template <int D, int BLK>
+__device__ __forceinline__ void merge_weights(const float* p0, int r, int nc, float& m,
+                                              float& rcp) {
+  constexpr int64_t S = BLK * D + 2 * BLK;
+  constexpr int G = 4;  // chunks per group of loads
+  m = -INFINITY;
+#pragma unroll
+  for (int c0 = 0; c0 < kMaxChunks; c0 += G) {
+    if (c0 >= nc) break;
+    float mc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) mc[g] = c0 + g < nc ? p0[(c0 + g) * S + BLK * D + r] : -INFINITY;
+#pragma unroll
+    for (int g = 0; g < G; ++g) m = fmaxf(m, mc[g]);
+  }
+  float lsum = 0.0f;
+#pragma unroll
+  for (int c0 = 0; c0 < kMaxChunks; c0 += G) {
+    if (c0 >= nc) break;
+    float mc[G], lc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      mc[g] = c0 + g < nc ? p0[(c0 + g) * S + BLK * D + r] : -INFINITY;
+      lc[g] = c0 + g < nc ? p0[(c0 + g) * S + BLK * D + BLK + r] : 0.0f;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      if (c0 + g < nc) lsum += __builtin_amdgcn_exp2f(mc[g] - m) * lc[g];
+  }
+  rcp = 1.0f / lsum;
+}
+
+// NX dims of query row r starting at dim x: sum_c w_c acc_c / sum_c w_c l_c,
+// stored to op in the output type. The chunks are taken four at a time, every
+// load of a group issued before any is used.
+template <typename T, int D, int BLK, int NX>
+__device__ __forceinline__ void merge_slice(const float* p0, int r, int x, int nc, float m,
+                                            float rcp, uint16_t* op) {
+  constexpr int64_t S = BLK * D + 2 * BLK;
+  constexpr int G = 4;
+  float4 acc[NX / 4];
+#pragma unroll
+  for (int q = 0; q < NX / 4; ++q) acc[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int c0 = 0; c0 < nc; c0 += G) {
+    float wc[G];
+    float4 oc[G][NX / 4];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const bool on = c0 + g < nc;
+      const float* pc = p0 + (c0 + g) * S;
+      wc[g] = on ? pc[BLK * D + r] : -INFINITY;
+#pragma unroll
+      for (int q = 0; q < NX / 4; ++q)
+        oc[g][q] = on ? *reinterpret_cast<const float4*>(pc + static_cast<int64_t>(r) * D + x + 4 * q)
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float w = c0 + g < nc ? __builtin_amdgcn_exp2f(wc[g] - m) : 0.0f;
+#pragma unroll
+      for (int q = 0; q < NX / 4; ++q) {
+        acc[q].x += w * oc[g][q].x;
+        acc[q].y += w * oc[g][q].y;
+        acc[q].z += w * oc[g][q].z;
+        acc[q].w += w * oc[g][q].w;
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < NX / 4; ++q) {
+    uint2 pk;
+    pk.x = pack2<T>(acc[q].x * rcp, acc[q].y * rcp);
+    pk.y = pack2<T>(acc[q].z * rcp, acc[q].w * rcp);
+    *reinterpret_cast<uint2*>(op + 4 * q) = pk;
   }
 }
 
@@ -766,14 +853,11 @@ __global__ __launch_bounds__(2 * BLK, D > 128 ? 1 : 2) void k_attn(AttnArgs a) {
 // Output rows of the split rows. Workgroup (slot, s) of the grid
 // (unit_slots x BLK / 32) takes query rows 32 s .. 32 s + 31 of the unit that
 // k_attn's chunk slot `slot` ran; only a row's first chunk's slots work. Eight
-// threads per query row, D / 8 dims each: every load of a thread (the chunks'
-// m and l, then its slice of each chunk's O) is issued before any is used, so
-// the merge costs about one memory latency. Flash-decoding merge:
-// m = max_c m_c, w_c = exp2(m_c - m), O = sum_c w_c acc_c / sum_c w_c l_c.
+// threads per query row, D / 8 dims each (merge_weights, then merge_slice:
+// about one memory latency per four chunks).
 template <typename T, int D, int BLK>
 __global__ __launch_bounds__(256) void k_merge(AttnArgs a) {
   constexpr int XT = D / 8;        // dims per thread
-  constexpr int MAXC = 4;          // chunks per split row (host policy)
   const int slot = static_cast<int>(blockIdx.x / (BLK / 32));
   const int s = static_cast<int>(blockIdx.x % (BLK / 32));
   int u, h;
@@ -783,53 +867,17 @@ __global__ __launch_bounds__(256) void k_merge(AttnArgs a) {
   const UnitRec ur =
       sld(reinterpret_cast<const UnitRec*>(reinterpret_cast<const char*>(a.units) + 64) + u);
   if (ur.c != 0) return;
-  const int nc = min(min(ur.nc, nunits - u), MAXC);
+  const int nc = min(min(ur.nc, nunits - u), kMaxChunks);
   const int r = 32 * s + static_cast<int>(threadIdx.x >> 3);
   const int x0 = XT * static_cast<int>(threadIdx.x & 7);
   const int qg = ur.r.i * BLK + r;
   if (qg >= ur.r.L) return;
-  const int64_t S = BLK * D + 2 * BLK;  // floats per partial
-  const float* p0 = a.part + (static_cast<int64_t>(h) * a.unit_cap + u) * S;
-  float mc[MAXC], lc[MAXC];
-#pragma unroll
-  for (int c = 0; c < MAXC; ++c) {
-    mc[c] = c < nc ? p0[c * S + BLK * D + r] : -INFINITY;
-    lc[c] = c < nc ? p0[c * S + BLK * D + BLK + r] : 0.0f;
-  }
-  float4 oc[MAXC][XT / 4];
-#pragma unroll
-  for (int c = 0; c < MAXC; ++c)
-#pragma unroll
-    for (int q = 0; q < XT / 4; ++q)
-      oc[c][q] = c < nc ? *reinterpret_cast<const float4*>(p0 + c * S + static_cast<int64_t>(r) * D +
-                                                          x0 + 4 * q)
-                        : make_float4(0.f, 0.f, 0.f, 0.f);
-  float m = mc[0];
-#pragma unroll
-  for (int c = 1; c < MAXC; ++c) m = fmaxf(m, mc[c]);
-  float wc[MAXC], lsum = 0.0f;
-#pragma unroll
-  for (int c = 0; c < MAXC; ++c) {
-    wc[c] = c < nc ? __builtin_amdgcn_exp2f(mc[c] - m) : 0.0f;
-    lsum += wc[c] * lc[c];
-  }
-  const float rcp = 1.0f / lsum;
+  const float* p0 =
+      a.part + (static_cast<int64_t>(h) * a.unit_cap + u) * static_cast<int64_t>(BLK * D + 2 * BLK);
+  float m, rcp;
+  merge_weights<D, BLK>(p0, r, nc, m, rcp);
   uint16_t* op = a.o + (ur.r.t0 + qg) * a.ost + static_cast<int64_t>(h) * a.ohs + x0;
-#pragma unroll
-  for (int q = 0; q < XT / 4; ++q) {
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int c = 0; c < MAXC; ++c) {
-      acc.x += wc[c] * oc[c][q].x;
-      acc.y += wc[c] * oc[c][q].y;
-      acc.z += wc[c] * oc[c][q].z;
-      acc.w += wc[c] * oc[c][q].w;
-    }
-    uint2 pk;
-    pk.x = pack2<T>(acc.x * rcp, acc.y * rcp);
-    pk.y = pack2<T>(acc.z * rcp, acc.w * rcp);
-    *reinterpret_cast<uint2*>(op + 4 * q) = pk;
-  }
+  merge_slice<T, D, BLK, XT>(p0, r, x0, nc, m, rcp, op);
 }
 
 template <typename T, int D>

@@ -144,18 +144,36 @@ int layout(const fp_problem* p, fp_ws_layout* L) {
   L->rowrec_off = off;     off = align_up(off + 16 * Hq * cap);
   L->idx_off = off;        off = align_up(off + 4 * Hq * tri);
   // Split rows (16-bit inputs, fp::UnitRec): a last_n row selects every causal
-  // block, so with one workgroup per row it outlasts the rest of the attention
-  // at short and mid lengths. Rows of more than C = max(8, ceil(NB / 4))
-  // blocks run as up to 4 chunks of C blocks; at most min(B, cap / (C + 1))
-  // sequences have more than C blocks. Each chunk unit keeps fp32 partials
-  // per query head (blk * d + 2 * blk floats), and their region is held to
-  // kSplitPartialBytes: a batch whose units would need more has enough long
-  // rows to balance the attention grid without splitting (one 4K sequence at
-  // 32 heads needs 17 MB; 256 sequences of 4K tokens would need 4.4 GB).
+  // block, so with one workgroup per row it can outlast the rest of the
+  // attention. Rows of more than C blocks run as chunks of at most C blocks.
+  // C is about one workgroup slot's share of the attention, estimated from
+  // below before the selection exists: every row's forced blocks (sink,
+  // window and min_budget; at least the diagonal) plus the last_n rows' full
+  // lists, over the resident slots of an MI355X (256 CUs; the count only sets
+  // the balance). A chunk longer than a slot's share becomes the kernel's
+  // critical path (one TP = 8 shard of a 128K sequence, 4 q / 1 kv heads:
+  // attention 0.80 ms with 256-block chunks, 0.74 ms with 64); a much shorter
+  // one adds per-chunk work (first loads, partial store, merge; 16-block
+  // chunks made the same shard at 32K 4 % slower than 64). C is at least 8
+  // and gives at most kMaxChunks chunks, evened out over the longest row
+  // (Llama shapes, 32 heads: two chunks from 4K on, 4K call -5 %). At most
+  // min(B, cap / (C + 1)) sequences have more than C blocks. Each chunk unit
+  // keeps fp32 partials per query head (blk * d + 2 * blk floats), and their
+  // region is held to kSplitPartialBytes: a batch whose units would need more
+  // has enough long rows to balance the attention grid without splitting.
   constexpr int64_t kSplitPartialBytes = int64_t(64) << 20;
+  constexpr int64_t kCUs = 256;
   int64_t split = 0, units = 0;
   if (p->dtype != FP_DTYPE_F32 && p->last_n_block > 0) {
-    split = std::max<int64_t>(8, (nb_max + 3) / 4);
+    const int64_t slots = kCUs * ((blk == 128 ? 2 : 4) / (d == 256 ? 2 : 1));
+    const int64_t forced = std::min<int64_t>(
+        nb_max, std::max<int64_t>(1, static_cast<int64_t>(std::max(p->attention_sink, 0)) +
+                                         std::max(p->window_size, 0) + std::max(p->min_budget, 0)));
+    const int64_t work = Hq * cap * (forced + std::min<int64_t>(p->last_n_block, nb_max));
+    split = std::max<int64_t>({8, (work + slots - 1) / slots,
+                               (nb_max + fp::kMaxChunks - 1) / fp::kMaxChunks});
+    const int64_t nchunks = (nb_max + split - 1) / split;
+    split = std::max<int64_t>(8, (nb_max + nchunks - 1) / nchunks);
     if (nb_max > split) {
       const int64_t seqs = std::min<int64_t>(B, cap / (split + 1));
       const int64_t rows = seqs * std::min<int64_t>(p->last_n_block, nb_max);
@@ -372,10 +390,12 @@ int run_attn(const fp_problem* p, const fp_ws_layout& L, void* ws, hipStream_t s
   // The chunks of a split row combine their partials themselves (the last to
   // finish reads the others' from L2) when they all run on one XCD: with Hq a
   // multiple of 8 the unit slots of head h are the slots of XCD h / (Hq / 8)
-  // (map_item), which share one L2. Otherwise k_merge runs after the
-  // attention.
+  // (map_item), which share one L2; and when a row has at most
+  // kMaxInlineChunks chunks. Otherwise k_merge runs after the attention.
   a.arrivals = arrival_counters(p, L, ws);
-  a.merge_inline = p->num_q_heads % 8 == 0 ? 1 : 0;
+  const int64_t max_chunks =
+      L.split_blocks > 0 ? (L.nb_max + L.split_blocks - 1) / L.split_blocks : 0;
+  a.merge_inline = p->num_q_heads % 8 == 0 && max_chunks <= fp::kMaxInlineChunks ? 1 : 0;
   a.ratio = block_ratio(p);
   const int blk = plan_block(p);
   hipError_t e;

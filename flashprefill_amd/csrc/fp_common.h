@@ -14,6 +14,8 @@ constexpr int kWave = 64;
 constexpr int kMaxBatch = 4096;   // sequences per call (plan kernel keeps them in LDS)
 constexpr int kMaxBlocks = 8192;  // blocks per sequence (1,048,576 tokens at block 128)
 constexpr int kSmallPlanBatch = 16;  // batches planned inside the pooling launch (k_plan_pool)
+constexpr int kMaxChunks = 8;        // chunks of one split row (host policy, k_merge)
+constexpr int kMaxInlineChunks = 8;  // chunks merged inside the attention kernel
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));

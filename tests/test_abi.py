@@ -72,16 +72,28 @@ def test_layout_bounds():
 
 
 def test_split_row_policy():
-    # last_n rows select every causal block; rows longer than C = max(8, ceil(NB / 4))
-    # blocks run as chunks of C (at most 4 per row) on 16-bit inputs
-    rc, L = _layout(_problem())  # 3 sequences, NB <= 32: C = 8, 3 x 2 rows x 4 chunks
+    # last_n rows select every causal block; on 16-bit inputs rows longer than C
+    # blocks run as chunks of at most C, where C is about one resident slot's
+    # share of a lower bound of the attention's blocks (forced blocks of every
+    # row plus the last_n rows' full lists over 512 slots at block 128), at
+    # least 8 and at most 8 chunks per row, evened out over the longest row
+    rc, L = _layout(_problem())  # 3 sequences, NB <= 32, 8 heads: C = 8, 3 x 2 rows x 4 chunks
     assert rc == _lib.FP_OK and L.split_blocks == 8 and L.unit_cap == 24
-    S = 131072
-    one = dict(batch=1, max_seq_len=S, total_tokens=S, num_q_heads=32, num_kv_heads=8,
-               q_stride_tok=32 * 128, k_stride_tok=8 * 128, v_stride_tok=8 * 128,
-               o_stride_tok=32 * 128)
-    rc, L = _layout(_problem(**one))
-    assert rc == _lib.FP_OK and L.split_blocks == 256 and L.unit_cap == 2 * 4
+
+    def one(S, hq, hkv):
+        return dict(batch=1, max_seq_len=S, total_tokens=S, num_q_heads=hq, num_kv_heads=hkv,
+                    q_stride_tok=hq * 128, k_stride_tok=hkv * 128, v_stride_tok=hkv * 128,
+                    o_stride_tok=hq * 128)
+    # 32 heads: 4K rows of 32 blocks in two chunks (32 x 32 x (6 + 2) / 512 = 16 blocks a
+    # slot), 128K in two chunks of 512
+    rc, L = _layout(_problem(**one(4096, 32, 8)))
+    assert rc == _lib.FP_OK and L.split_blocks == 16 and L.unit_cap == 2 * 2
+    rc, L = _layout(_problem(**one(131072, 32, 8)))
+    assert rc == _lib.FP_OK and L.split_blocks == 512 and L.unit_cap == 2 * 2
+    # one TP = 8 shard of 128K (4 q / 1 kv head): a slot's share is 64 blocks, so the
+    # dense rows run as 8 chunks (the most) instead of being the kernel's critical path
+    rc, L = _layout(_problem(**one(131072, 4, 1)))
+    assert rc == _lib.FP_OK and L.split_blocks == 128 and L.unit_cap == 2 * 8
     for off in (dict(dtype=_lib.FP_DTYPE_F32), dict(last_n_block=0),
                 dict(max_seq_len=1024, total_tokens=3 * 1024)):  # fp32, no dense rows, NB <= 8
         rc, L = _layout(_problem(**off))
@@ -155,6 +167,7 @@ def test_split_units_never_exceed_the_capacity():
     rnd = random.Random(5)
     for trial in range(300):
         B = rnd.choice([1, 2, 3, 5, 17])
+        hq = rnd.choice([2, 8, 32])
         block = rnd.choice([64, 128])
         max_len = rnd.choice([700, 2048, 5000, 20000])
         lens = [rnd.randint(0, max_len) for _ in range(B)]
@@ -162,7 +175,9 @@ def test_split_units_never_exceed_the_capacity():
         last_n = rnd.choice([1, 2, 3, 7])
         T = sum(lens) + rnd.randint(0, 300)
         rc, L = _layout(_problem(batch=B, max_seq_len=max_len, total_tokens=T,
-                                 block_size=block, last_n_block=last_n))
+                                 block_size=block, last_n_block=last_n, num_q_heads=hq,
+                                 num_kv_heads=2 if hq > 2 else 1, q_stride_tok=hq * 128,
+                                 o_stride_tok=hq * 128))
         assert rc == _lib.FP_OK
         C = L.split_blocks
         n = 0
@@ -170,7 +185,7 @@ def test_split_units_never_exceed_the_capacity():
             nb = -(-Ls // block)
             for i in range(max(nb - last_n, 0), nb):
                 if C > 0 and i + 1 > C:
-                    assert -(-(i + 1) // C) <= 4  # the merge kernel combines at most 4
+                    assert -(-(i + 1) // C) <= 8  # the merges combine at most 8
                     n += -(-(i + 1) // C)
         assert n <= L.unit_cap, (lens, block, last_n, C, n, L.unit_cap)
 

@@ -1,9 +1,14 @@
 """Parity of the split-row path: the last_n rows of a sequence select every
 causal block, and rows longer than the host's chunk size run as chunk
-workgroups whose fp32 partials the merge kernel combines. Ragged batches with
-several split sequences (bf16 / block 128 and fp16 / d 64 / block 64, last_n
-above 2) go through every stage against the oracle, the full attention output
-included, after checking that the plan emitted the expected chunk units."""
+workgroups whose fp32 partials are merged (by the row's last chunk inside the
+attention kernel when Hq is a multiple of 8, else by k_merge). Ragged batches
+with several split sequences (bf16 / block 128 and fp16 / d 64 / block 64,
+last_n above 2) go through every stage against the oracle, the full attention
+output included, after checking that the plan emitted the expected chunk
+units. Few heads over a long sequence (a tensor-parallel shard) make the
+chunks short and many (8 per dense row, the most, merged by k_merge and
+inside the kernel); those cases check sampled rows against the oracle and
+every row against the closed form."""
 
 import pytest
 import torch
@@ -63,6 +68,28 @@ def test_split_rows_match_oracle(lens, Hq, Hkv, d, dtype, block, last_n, seed):
     rep = run_stages(q, k, v, cu, max(lens), alpha=0.18, last_n=last_n, block=block)
     print(f"  e2e_flips={rep.e2e_flips}/{rep.cells} out_max={rep.out_max_abs:.2e} "
           f"out_mean={rep.out_mean_abs:.2e}", flush=True)
+    assert rep.sel_from_gpu_scores_mismatch == 0
+    assert rep.sel_from_oracle_scores_mismatch == 0
+    assert rep.e2e_flips <= max(2, 2e-3 * rep.cells)
+    assert rep.out_max_abs <= OUT_MAX_ABS
+    assert rep.out_mean_abs <= OUT_MEAN_ABS
+
+
+@pytest.mark.parametrize("S,Hq,Hkv,want_chunks,seed", [
+    (32768, 4, 1, 8, 13),    # Hq % 8 != 0: k_merge combines 8 partials per row
+    (16384, 8, 2, 8, 14),    # Hq % 8 == 0: the row's last chunk merges 8 partials
+])
+def test_many_chunks_per_row(S, Hq, Hkv, want_chunks, seed):
+    q, k, v, cu = _inputs([S], Hq, Hkv, 128, torch.bfloat16, seed)
+    C, cap, n = _planned_units(q, k, v, cu, 128, 2)
+    nb = S // 128
+    print(f"\n  S={S} Hq={Hq}: chunk size {C} blocks, {n} units planned", flush=True)
+    assert -(-nb // C) == want_chunks and n == _expected_units([S], 128, 2, C) <= cap
+    rows = {0: [(0, nb - 1), (Hq - 1, nb - 2), (Hq // 2, nb // 2), (1, 3)]}
+    rep = run_stages(q, k, v, cu, S, alpha=0.18, last_n=2, attn_rows=rows)
+    print(f"  e2e_flips={rep.e2e_flips}/{rep.cells} out_max={rep.out_max_abs:.2e} "
+          f"out_mean={rep.out_mean_abs:.2e} rows checked={rep.full_rows}", flush=True)
+    assert rep.full_rows > 0
     assert rep.sel_from_gpu_scores_mismatch == 0
     assert rep.sel_from_oracle_scores_mismatch == 0
     assert rep.e2e_flips <= max(2, 2e-3 * rep.cells)
