@@ -643,12 +643,20 @@ def config_cases(config):
     if config == 4:
         return [(synth.qwen_varlen_spec(), 0.08,
                  "ragged {256K, 64K, 17K, 3K, 1K}, Qwen2.5-7B heads")]
+    if config == "tp":
+        # one rank's share of config 3 under tensor parallelism over heads
+        # (what vLLM runs, README.md:33): 32 / TP query and 8 / TP KV heads at
+        # the full 128K length, for TP = 8 and 4
+        return [(synth.SynthSpec(seq_lens=(131072,), num_q_heads=32 // tp, num_kv_heads=8 // tp,
+                                 head_dim=128, seed=128), 0.18,
+                 f"128K, one TP = {tp} rank ({32 // tp} q / {8 // tp} kv heads)") for tp in (8, 4)]
     raise SystemExit(f"--config {config}: 1, 2, 3, 4 or 5")
 
 
 def config_results(config, steps, warmup, dense):
     """Configs 2 (Llama shapes at 4K / 16K / 32K) and 4 (Qwen2.5 varlen
-    ragged batch): one result per case."""
+    ragged batch), config 3 at 256K and one tensor-parallel rank's share of
+    config 3 ("tp"): one result per case."""
     import torch
     from flashprefill_amd import synth
     dev = torch.device("cuda:0")
@@ -918,6 +926,8 @@ def main():
         for c in (2, 4):
             configs[f"config_{c}"] = config_results(c, sub_steps, sub_warmup, not args.no_dense)
         configs["config_3_256k"] = config_results(3, sub_steps, sub_warmup, not args.no_dense)
+        configs["config_3_tp_ranks"] = config_results("tp", sub_steps, sub_warmup,
+                                                      not args.no_dense)
         print("bench: config 5", file=sys.stderr, flush=True)
         sub = argparse.Namespace(steps=sub_steps, warmup=sub_warmup, no_dense=args.no_dense)
         configs["config_5"] = decoder_layer_report(sub)
