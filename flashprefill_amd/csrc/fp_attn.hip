@@ -244,15 +244,17 @@ __device__ __forceinline__ void attn_block(AttnState<T, D>& st, const typename T
   }
 }
 
-// d = 256: one selected block in two passes of KP = 2 key tiles (64 keys)
-// each: S, the online softmax and O += V^T.P^T per pass, so that a pass's S
-// and P (32 + 16 registers) sit beside the 128 output accumulators and the
-// 64 query-operand registers of a wave. This is the online softmax over
-// 64-key tiles (the reference's other K_TILE_SIZE), a rounding-level
-// difference from one 128-key tile. The K refill follows the last pass's S,
-// the V refill the last pass's P.V; the V wait precedes the first pass's P.V.
+// d = 256: one selected block in passes of KP 32-key tiles: S, the online
+// softmax and O += V^T.P^T per pass, so that a pass's S and P (16 + 8
+// registers at KP = 1) sit beside the 128 output accumulators and the 64
+// query-operand registers of a wave. (At KP = 2 the compiler spilled ~50
+// registers to scratch memory and the attention was 14-16 % slower.) This is
+// the online softmax over 32-key tiles, a rounding-level difference from the
+// reference's 64- or 128-key K_TILE_SIZE. The K refill follows the last
+// pass's S, the V refill the last pass's P.V; the V wait precedes the first
+// pass's P.V.
 template <typename T, int D, int BLK, bool DIAG>
-__device__ __forceinline__ void attn_block_2pass(AttnState<T, D>& st, const typename T::vec8* qb,
+__device__ __forceinline__ void attn_block_passes(AttnState<T, D>& st, const typename T::vec8* qb,
                                                  const uint4* sk, uint4* sk_w,
                                                  const uint16_t* sv16, uint4* sv_w,
                                                  const uint16_t* kbase, const uint16_t* vbase,
@@ -265,7 +267,7 @@ __device__ __forceinline__ void attn_block_2pass(AttnState<T, D>& st, const type
   constexpr int KS = D / 16;
   constexpr int DT = D / 32;
   constexpr int KT = BLK / 32;  // 32-key tiles of S^T per block
-  constexpr int KP = 2;         // key tiles per pass
+  constexpr int KP = 1;         // key tiles per pass
   constexpr int NP = KT / KP;   // passes
   constexpr int NW = BLK / 32;
   static_assert(KT % KP == 0, "whole passes");
@@ -708,7 +710,7 @@ __device__ __forceinline__ bool attn_slot(const Args& a, int slot, int t, Tail t
   for (int n = 0; n < nplain; ++n) {
     const int jn = n + 1 < ncnt ? min(max(jraw, 0), i) : -1;
     if constexpr (D > 128) {
-      attn_block_2pass<T, D, BLK, false>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk,
+      attn_block_passes<T, D, BLK, false>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk,
                                          tv, jn, list + min(n + 2, ncnt - 1), jraw, L, c, n == 0,
                                          w, lane);
     } else {
@@ -719,7 +721,7 @@ __device__ __forceinline__ bool attn_slot(const Args& a, int slot, int t, Tail t
   if (has_diag) {
     int unused;
     if constexpr (D > 128) {
-      attn_block_2pass<T, D, BLK, true>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk,
+      attn_block_passes<T, D, BLK, true>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk,
                                         tv, -1, list, unused, L, c, nplain == 0, w, lane);
     } else {
       attn_block<T, D, BLK, true>(st, qb, sk, sk, sv16, sv, kbase, vbase, a.kst, a.vst, tk, tv, -1,
@@ -788,7 +790,7 @@ __device__ __forceinline__ bool attn_slot(const Args& a, int slot, int t, Tail t
 // BLK = 128: 4 waves, 64 KB of LDS (d = 128), two workgroups per CU;
 // BLK = 64: 2 waves, 32 KB, four workgroups per CU. Either way two waves per
 // SIMD (the second launch bound is waves per execution unit), i.e. at most
-// 256 registers per wave. At d = 256 (two passes per block) the output
+// 256 registers per wave. At d = 256 (32-key passes per block) the output
 // accumulators take 128 registers and the query operands 64: a wave runs
 // alone on its SIMD (up to 512 registers, VGPRs and AGPRs), one workgroup
 // per CU at BLK = 128 (128 KB of LDS), two at BLK = 64.

@@ -284,7 +284,9 @@ def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n
         for b, (s0, s1) in enumerate(seq_slices(cu_list)):
             if s1 == s0:
                 continue
-            # the attention walks 128-key tiles (64-key passes at head_dim 256)
+            # the attention walks 128-key tiles; at head_dim 256 it takes each
+            # block in 32-key passes, and the oracle uses the reference's
+            # K_TILE_SIZE 64 there (the two differ at rounding level)
             k_tile = 64 if q.shape[-1] > 128 else min(block, 128)
             if attn_rows is None:
                 ref = O.sparse_attention(q[s0:s1], k[s0:s1], v[s0:s1], gpu_sel[b], block, k_tile)
