@@ -69,6 +69,23 @@ def test_qwen_heads_not_multiple_of_8_fp16_d64():
     _check(run_stages(q, k, v, cu, 1000, alpha=0.08))
 
 
+@pytest.mark.parametrize("hq,hkv", [(12, 3), (24, 6)])
+def test_kv_heads_not_dividing_8(hq, hkv):
+    # KV head counts that do not divide the 8 XCDs: rows map head-major
+    # (map_item) instead of by GQA group sets; sizes that run the persistent
+    # attention grid, sampled rows against the oracle and every row against
+    # the closed form
+    lens = (20000, 3000, 129)
+    spec = synth.SynthSpec(seq_lens=lens, num_q_heads=hq, num_kv_heads=hkv, head_dim=128,
+                           seed=60 + hkv)
+    q, k, v, cu = synth.make_inputs(spec)
+    nbs = [(n + 127) // 128 for n in lens]
+    rows = {b: [(0, nb - 1), (hq - 1, nb // 2), (hq // 2, 0)] for b, nb in enumerate(nbs)}
+    rep = run_stages(q, k, v, cu.tolist(), max(lens), alpha=0.18, attn_rows=rows)
+    assert rep.full_rows > 0
+    _check(rep)
+
+
 @pytest.mark.parametrize("min_budget", [3, 40])
 def test_native_min_budget(min_budget):
     # the min_budget largest scores of a row are forced on (native path,
