@@ -8,6 +8,7 @@ import re
 from pathlib import Path
 
 import pytest
+import torch
 
 from flashprefill_amd import _lib
 
@@ -342,3 +343,17 @@ def test_plan_rule_bound_holds_for_arbitrary_cu_seqlens():
         assert rc == _lib.FP_OK
         nb_sum, tri_sum = _plan_block_count(cu, T, max_len)
         assert nb_sum <= L.nb_sum_cap and tri_sum <= L.tri_cap, (cu, T, max_len)
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    # the GPU path has no CPU fallback: without the built library loading it
+    # raises, and CPU tensors are refused rather than computed some other way
+    monkeypatch.setattr(_lib, "_LIB", None)
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.load(tmp_path / "libflashprefill.so")
+    from flashprefill_amd import flash_prefill_varlen_func
+    q = torch.zeros(4, 2, 64, dtype=torch.bfloat16)
+    kv = torch.zeros(4, 1, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        flash_prefill_varlen_func(q, kv, kv, torch.empty_like(q),
+                                  torch.tensor([0, 4], dtype=torch.int32), 4, 0.18)
