@@ -49,8 +49,10 @@ class StageReport:
     sel_from_oracle_scores_mismatch: int = 0
     e2e_flips: int = 0
     cells: int = 0
-    out_max_abs: float = 0.0
-    out_mean_abs: float = 0.0
+    out_max_abs: float = 0.0        # over the elements whose output spacing is within the bar
+    out_mean_abs: float = 0.0       # over every element
+    out_coarse: int = 0             # elements whose output spacing exceeds the bar (|ref| >= 4 in bf16)
+    out_coarse_ulp: int = 0         # max ulp distance over those (at most 1)
     density: float = 0.0
     full_rows: int = 0              # (head, q-block) rows checked against the GPU closed form
     notes: List[str] = field(default_factory=list)
@@ -69,6 +71,34 @@ def pool_errors(mk_gpu: torch.Tensor, mk_o: torch.Tensor):
     worst = (f"element {i}: gpu {mk_gpu.reshape(-1)[i].item():.8g} "
              f"oracle {mk_o.reshape(-1)[i].item():.8g} ({int(dist[i])} ulp)")
     return int(dist[i]), int((dist != 0).sum()), worst
+
+
+def output_spacing(ref: torch.Tensor) -> torch.Tensor:
+    """Spacing of ref's dtype at |ref| (one unit in the last place; zero and
+    subnormals get the spacing at the smallest normal)."""
+    fi = torch.finfo(ref.dtype)
+    mant = {torch.bfloat16: 7, torch.float16: 10, torch.float32: 23}[ref.dtype]
+    a = ref.float().abs().clamp_min(fi.tiny)
+    return torch.exp2(torch.floor(torch.log2(a)) - mant)
+
+
+def output_errors(out: torch.Tensor, ref: torch.Tensor, bar: float):
+    """Element errors of an output against the oracle's, both rounded to the
+    same dtype. Where that dtype's spacing at |ref| exceeds the max-abs bar
+    (bf16 at |ref| >= 4, spacing 2^-5 = 0.031 > 2e-2), two results that each
+    round a nearly equal fp32 value can differ by one spacing from the final
+    rounding alone, so such "coarse" elements are held to <= 1 ulp instead;
+    the bar applies to every other element. Returns (abs errors of the
+    bar-checked elements, abs errors of every element, number of coarse
+    elements, max ulp distance among them)."""
+    d = (out.float() - ref.float()).abs().reshape(-1)
+    coarse = (output_spacing(ref) > bar).reshape(-1)
+    n = int(coarse.sum())
+    ulp = 0
+    if n:
+        dist = (_ulp_line(out.reshape(-1)[coarse]) - _ulp_line(ref.reshape(-1)[coarse])).abs()
+        ulp = int(dist.max())
+    return d[~coarse], d, n, ulp
 
 
 def assert_pool(rep: StageReport) -> None:
@@ -280,7 +310,16 @@ def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n
         call.attn()
         torch.cuda.synchronize()
         out = od.cpu()
-        diffs = []
+        f32 = q.dtype == torch.float32
+        bar = OUT_MAX_ABS_F32 if f32 else OUT_MAX_ABS
+        diffs, diffs_all = [], []
+
+        def add(o, r):
+            dm, da, n, ulp = output_errors(o, r, bar)
+            diffs.append(dm)
+            diffs_all.append(da)
+            rep.out_coarse += n
+            rep.out_coarse_ulp = max(rep.out_coarse_ulp, ulp)
         for b, (s0, s1) in enumerate(seq_slices(cu_list)):
             if s1 == s0:
                 continue
@@ -290,7 +329,7 @@ def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n
             k_tile = 64 if q.shape[-1] > 128 else min(block, 128)
             if attn_rows is None:
                 ref = O.sparse_attention(q[s0:s1], k[s0:s1], v[s0:s1], gpu_sel[b], block, k_tile)
-                diffs.append((out[s0:s1].float() - ref.float()).abs().reshape(-1))
+                add(out[s0:s1], ref)
                 continue
             sub = torch.zeros_like(gpu_sel[b])
             for h, i in attn_rows.get(b, []):
@@ -298,12 +337,13 @@ def run_stages(q, k, v, cu_list, max_seq_len, *, alpha, sink=2, window=4, last_n
             ref = O.sparse_attention(q[s0:s1], k[s0:s1], v[s0:s1], sub, block, k_tile)
             for h, i in attn_rows.get(b, []):
                 r0, r1 = i * block, min((i + 1) * block, s1 - s0)
-                diffs.append((out[s0 + r0:s0 + r1, h].float() - ref[r0:r1, h].float())
-                             .abs().reshape(-1))
-        d = torch.cat(diffs)
-        assert not torch.isnan(d).any(), "NaN in GPU output"
-        rep.out_max_abs = d.max().item()
-        rep.out_mean_abs = d.mean().item()
+                add(out[s0 + r0:s0 + r1, h], ref[r0:r1, h])
+        d, d_all = torch.cat(diffs), torch.cat(diffs_all)
+        assert not torch.isnan(d_all).any(), "NaN in GPU output"
+        assert rep.out_coarse_ulp <= 1, \
+            f"{rep.out_coarse_ulp} ulp on an output element whose spacing exceeds {bar}"
+        rep.out_max_abs = d.max().item() if d.numel() else 0.0
+        rep.out_mean_abs = d_all.mean().item()
         if attn_rows is not None:
             # the oracle saw sampled rows only: every row against the closed
             # form on the GPU, from the same lists, under the same bars

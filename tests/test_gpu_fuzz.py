@@ -53,7 +53,10 @@ def _case(seed):
     return lens, hq, hkv, d, dtype, params, shape, block
 
 
-@pytest.mark.parametrize("seed", range(24))
+# seeds 50 and 130 (and 53, 56, 91, 105 of the wide set) reach outputs of
+# magnitude >= 4, where a bf16 ulp (2^-5) exceeds the max-abs bar and the
+# parity helper holds elements to one ulp (output_errors)
+@pytest.mark.parametrize("seed", list(range(24)) + [50, 130])
 def test_random_configuration(seed):
     lens, hq, hkv, d, dtype, params, shape, block = _case(1000 + seed)
     g = torch.Generator().manual_seed(seed)
@@ -80,7 +83,8 @@ def test_random_configuration(seed):
           f"{shape}", flush=True)
     rep = run_stages(q, k, v, cu, max(lens), block=block, **params)
     print(f"  flips={rep.e2e_flips}/{rep.cells} density={rep.density:.3f} "
-          f"out_max={rep.out_max_abs:.2e} out_mean={rep.out_mean_abs:.2e}", flush=True)
+          f"out_max={rep.out_max_abs:.2e} out_mean={rep.out_mean_abs:.2e} "
+          f"coarse={rep.out_coarse} ({rep.out_coarse_ulp} ulp)", flush=True)
     assert_pool(rep)
     assert rep.m_max_rel < 1e-4
     assert rep.p_max_rel < 1e-3
@@ -106,7 +110,7 @@ def _wide_case(seed):
     return lens, hq, hkv, d, dtype, params, shape, block
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", list(range(16)) + [53, 56, 91, 105])
 def test_random_configuration_wide_blocks_and_head_dims(seed):
     lens, hq, hkv, d, dtype, params, shape, block = _wide_case(3000 + seed)
     g = torch.Generator().manual_seed(300 + seed)
@@ -125,7 +129,8 @@ def test_random_configuration_wide_blocks_and_head_dims(seed):
           flush=True)
     rep = run_stages(q, k, v, cu, max(lens), block=block, **params)
     print(f"  flips={rep.e2e_flips}/{rep.cells} density={rep.density:.3f} "
-          f"out_max={rep.out_max_abs:.2e} out_mean={rep.out_mean_abs:.2e}", flush=True)
+          f"out_max={rep.out_max_abs:.2e} out_mean={rep.out_mean_abs:.2e} "
+          f"coarse={rep.out_coarse} ({rep.out_coarse_ulp} ulp)", flush=True)
     assert_pool(rep)
     assert rep.m_max_rel < 1e-4
     assert rep.p_max_rel < 1e-3
@@ -182,7 +187,8 @@ def test_random_large_configuration_persistent_attention(seed):
           flush=True)
     rep = run_stages(q, k, v, cu, max(lens), block=block, attn_rows=rows, **params)
     print(f"  flips={rep.e2e_flips}/{rep.cells} density={rep.density:.3f} "
-          f"out_max={rep.out_max_abs:.2e} out_mean={rep.out_mean_abs:.2e}", flush=True)
+          f"out_max={rep.out_max_abs:.2e} out_mean={rep.out_mean_abs:.2e} "
+          f"coarse={rep.out_coarse} ({rep.out_coarse_ulp} ulp)", flush=True)
     assert_pool(rep)
     assert rep.m_max_rel < 1e-4
     assert rep.p_max_rel < 1e-3

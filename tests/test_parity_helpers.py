@@ -2,13 +2,16 @@
 pool_errors / assert_pool): a block mean computed the way the pooling kernel
 computes it (fp64 row-group sums, fp64 division, cast through fp32) is bit
 equal to the oracle's, cancelling columns included; the same mean summed in
-fp32 fails the bar where the block mean cancels; a planted error fails."""
+fp32 fails the bar where the block mean cancels; a planted error fails. The
+output criterion (output_errors): the max-abs bar on elements whose output
+spacing is within it, one ulp on the others. The closed-form checker of every
+output row agrees with the oracle and catches planted mistakes."""
 
 import torch
 
 from oracle import flashprefill_oracle as O
-from tests._parity import (StageReport, assert_pool, every_row_vs_closed_form, pool_errors,
-                           ulp_diff_16)
+from tests._parity import (StageReport, assert_pool, every_row_vs_closed_form, output_errors,
+                           output_spacing, pool_errors, ulp_diff_16)
 
 
 def _kernel_pool(k: torch.Tensor, block: int, acc_dtype=torch.float64) -> torch.Tensor:
@@ -101,6 +104,48 @@ def test_signed_zeros_are_equal():
     a = torch.tensor([0.0, -0.0, 1.0], dtype=torch.bfloat16)
     b = torch.tensor([-0.0, 0.0, 1.0], dtype=torch.bfloat16)
     assert pool_errors(a, b)[:2] == (0, 0)
+
+
+def test_output_spacing_matches_the_dtypes():
+    for dt, mant in ((torch.bfloat16, 7), (torch.float16, 10), (torch.float32, 23)):
+        x = torch.tensor([1.0, 3.5, 4.0, 6.25, -5.0, 0.75], dtype=dt)
+        want = torch.tensor([2.0 ** (e - mant) for e in (0, 1, 2, 2, 2, -1)])
+        assert torch.equal(output_spacing(x), want), dt
+        # one step of the dtype up from x is x + spacing
+        step = (x.float() + want).to(dt)
+        assert torch.equal(_next_up(x), step), dt
+
+
+def _next_up(x):
+    # the next representable value of x's dtype above x (x > 0 or x < 0, finite)
+    i = x.view(torch.int16 if x.element_size() == 2 else torch.int32)
+    up = torch.where(x >= 0, i + 1, i - 1)  # sign-magnitude bit patterns
+    return up.view(x.dtype)
+
+
+def test_output_errors_hold_coarse_elements_to_one_ulp():
+    bar = 2e-2
+    ref = torch.tensor([0.5, 1.5, 3.9, 4.5, -6.0, 9.0], dtype=torch.bfloat16)
+    # every element one ulp up: only the coarse ones (|ref| >= 4, spacing
+    # 2^-5 and 2^-4 > bar) are exempt from the bar, and they are at 1 ulp
+    out = _next_up(ref)
+    main, every, n, ulp = output_errors(out, ref, bar)
+    assert n == 3 and ulp == 1
+    assert main.numel() == 3 and float(main.max()) == 2.0 ** -6  # 3.9: spacing 2^-6 < bar
+    assert every.numel() == 6 and float(every.max()) == 2.0 ** -4
+    # two ulps on a coarse element are reported as such
+    out2 = out.clone()
+    out2[3] = _next_up(out[3:4])[0]
+    assert output_errors(out2, ref, bar)[3] == 2
+    # below 4 the bar applies: 3.9 + 2 ulps (0.031) is above it
+    out3 = ref.clone()
+    out3[2] = _next_up(_next_up(ref[2:3]))[0]
+    main3 = output_errors(out3, ref, bar)[0]
+    assert float(main3.max()) > bar
+    # fp16 and fp32 outputs of this size have spacings far below the bar
+    for dt in (torch.float16, torch.float32):
+        r = ref.to(dt)
+        assert output_errors(_next_up(r), r, bar)[2] == 0
 
 
 class _ListsCall:
