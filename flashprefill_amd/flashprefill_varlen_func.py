@@ -50,7 +50,8 @@ def flash_prefill_varlen_func(
 
     Raises ValueError for malformed arguments and NotImplementedError for
     arguments the reference accepts but this build does not (head_dim other
-    than 64 / 128, block_size other than 64 / 128 / 256).
+    than 64 / 128 / 256, head_dim 256 with fp32 inputs or at block_size 256,
+    block_size other than 64 / 128 / 256).
     """
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     target = o

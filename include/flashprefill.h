@@ -226,7 +226,7 @@ typedef struct fp_rope_args {
     float eps;
     int32_t num_q_heads;
     int32_t num_kv_heads;
-    int32_t head_dim;         /* 64 or 128 */
+    int32_t head_dim;         /* 64, 128 or 256 */
     int32_t dtype;            /* FP_DTYPE_BF16 or FP_DTYPE_F16 */
 } fp_rope_args;
 int fp_rope_qk(const fp_rope_args* a, void* stream);
