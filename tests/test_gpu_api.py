@@ -268,3 +268,77 @@ def test_error_paths():
     with pytest.raises(NotImplementedError):  # head_dim 256 is built for 16-bit inputs
         flash_prefill_varlen_func(q256, q256[:, :1].contiguous(), q256[:, :1].contiguous(),
                                   q256.clone(), cu, T, 0.1)
+
+
+def _entry_case(seed):
+    """Random shapes for the whole-operator entry points: ragged varlen batches
+    with zero-length and 1-token sequences, or a batched native call with
+    min_budget; blocks 64 / 128 / 256, head_dims 64 / 128 / 256, fp32."""
+    import random
+    rnd = random.Random(7000 + seed)
+    block = rnd.choice([64, 128, 128, 256])
+    d = rnd.choice([64, 128, 128, 256])
+    dtype = rnd.choice([torch.bfloat16, torch.float16, torch.bfloat16])
+    if d == 256 and block == 256:
+        d = 128
+    if rnd.random() < 0.15 and d != 256 and block != 256:
+        dtype = torch.float32
+    hkv = rnd.choice([1, 2, 4, 8])
+    hq = hkv * rnd.choice([1, 2, 4, 7])
+    lens = [rnd.choice([0, 1, rnd.randint(2, 600), rnd.randint(600, 5000)])
+            for _ in range(rnd.randint(1, 5))]
+    if sum(lens) == 0:
+        lens[0] = 1
+    params = dict(alpha=rnd.choice([0.0, 0.05, 0.12, 0.18, 0.5]), sink=rnd.randint(0, 3),
+                  window=rnd.randint(0, 6), last_n=rnd.randint(0, 3))
+    native = rnd.random() < 0.3
+    min_budget = rnd.randint(1, 10) if native and rnd.random() < 0.5 else 0
+    return block, d, dtype, hq, hkv, lens, params, native, min_budget
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_whole_operator_entry_points_equal_the_staged_path(seed):
+    """The public entry points (plan and pooling in one launch for small
+    batches, cached workspace) write the same bits as the staged C-ABI calls
+    (plan, pool, search, attention) that the parity tests pin to the oracle."""
+    block, d, dtype, hq, hkv, lens, p, native, mb = _entry_case(seed)
+    print(f"\n  seed={seed} lens={lens} hq={hq} hkv={hkv} d={d} {dtype} block={block} {p} "
+          f"native={native} min_budget={mb}", flush=True)
+    bits = torch.int32 if dtype == torch.float32 else torch.int16
+    if not native:
+        T = sum(lens)
+        q, k, v = (_rand((T, hq, d), seed, dtype, 2.0), _rand((T, hkv, d), seed + 1, dtype, 2.0),
+                   _rand((T, hkv, d), seed + 2, dtype))
+        qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+        cu = torch.tensor([0] + torch.tensor(lens).cumsum(0).tolist(), dtype=torch.int32,
+                          device=DEV)
+        S = max(lens)
+        o_pub = torch.full_like(qd, 7.0)
+        flash_prefill_varlen_func(qd, kd, vd, o_pub, cu, S, p["alpha"], block, p["sink"],
+                                  p["window"], p["last_n"])
+        o_st = torch.full_like(qd, 7.0)
+        call = FlashPrefillCall(qd, kd, vd, o_st, cu, S, alpha=p["alpha"], attention_sink=p["sink"],
+                                window_size=p["window"], last_n_block=p["last_n"],
+                                block_size=block)
+    else:
+        B, L = min(len(lens), 3), max(max(lens), 1)
+        q = _rand((B, L, hq, d), seed, dtype, 2.0)
+        k, v = _rand((B, L, hkv, d), seed + 1, dtype, 2.0), _rand((B, L, hkv, d), seed + 2, dtype)
+        qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+        o4 = torch.full_like(qd, 7.0)
+        flash_prefill(qd, kd, vd, o4, block, p["sink"], p["window"], p["alpha"], p["last_n"], mb)
+        o_pub = o4.view(B * L, hq, d)
+        o_st = torch.full_like(o_pub, 7.0)
+        call = FlashPrefillCall(qd.view(B * L, hq, d), kd.view(B * L, hkv, d),
+                                vd.view(B * L, hkv, d), o_st, None, L, alpha=p["alpha"],
+                                attention_sink=p["sink"], window_size=p["window"],
+                                last_n_block=p["last_n"], native_normalize=True, min_budget=mb,
+                                block_size=block, batch=B, uniform_seq_len=L)
+    call.plan()
+    call.pool()
+    call.search()
+    call.attn()
+    torch.cuda.synchronize()
+    assert call.status() == 0
+    assert not torch.isnan(o_pub.float()).any()
+    assert torch.equal(o_pub.view(bits), o_st.view(bits))
