@@ -342,3 +342,37 @@ def test_whole_operator_entry_points_equal_the_staged_path(seed):
     assert call.status() == 0
     assert not torch.isnan(o_pub.float()).any()
     assert torch.equal(o_pub.view(bits), o_st.view(bits))
+
+
+def test_concurrent_calls_on_two_streams():
+    """Two public calls in flight at once on two streams (default priority),
+    each at a size where the attention runs as the persistent grid: each
+    stream takes its own cached workspace (so its own claim queues), and both
+    outputs equal those of the same calls made one after the other."""
+    from flashprefill_amd.runtime import release_workspaces
+    T, Hq, Hkv, d = 16384, 32, 8, 128
+    cu = torch.tensor([0, T], dtype=torch.int32, device=DEV)
+    ins = []
+    for s in (61, 71):
+        ins.append((_rand((T, Hq, d), s, scale=1.5).to(DEV), _rand((T, Hkv, d), s + 1, scale=1.5).to(DEV),
+                    _rand((T, Hkv, d), s + 2).to(DEV)))
+    refs = []
+    for q, k, v in ins:  # one after the other on the current stream
+        o = torch.empty_like(q)
+        flash_prefill_varlen_func(q, k, v, o, cu, T, 0.18)
+        refs.append(o)
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [torch.full_like(q, float("nan")) for q, _, _ in ins]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for (q, k, v), o, st in zip(ins, outs, streams):
+            o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        for (q, k, v), o, st in zip(ins, outs, streams):
+            with torch.cuda.stream(st):
+                flash_prefill_varlen_func(q, k, v, o, cu, T, 0.18)
+        torch.cuda.synchronize()
+        for o, r in zip(outs, refs):
+            assert torch.equal(o, r), rep
+    release_workspaces()
